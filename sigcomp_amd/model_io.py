@@ -1,0 +1,263 @@
+"""Checkpoint -> integer model contract of SigComp's quantised MLP.
+
+The integer model is what both reference backends derive from a PTQ
+checkpoint (``cpu_int_inference.py:395-445`` load_cpu_decoder and
+``quant_mlp_export.py:144-200`` convert_ptq_to_gpu_pipeline):
+
+* ``emb_q = clamp(round(E / s_in), -128, 127)`` (torch round, half to even);
+* per layer ``bias_q = round(b / (s_in * s_w))`` as int32 and
+  ``(M0, shift) = frexp(s_in * s_w / s_out)`` with ``M0 = round(sig * 2**31)``
+  and ``shift = 31 - exp``;
+* ReLU on every layer except the last; the last layer's output scale is
+  the logit scale from which the integer exp-LUT is built.
+
+The arithmetic is carried out with the same torch / float64 operations as
+the reference so that every constant is bit-identical.  The bundled models
+ship as ``.npz`` integer exports (``sigcomp_amd/pretrained``) written by
+``export_npz``; a ``.pth`` PTQ checkpoint is read with
+``torch.load(weights_only=True)`` and converted here.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from decimal import Decimal, localcontext
+from pathlib import Path
+
+import numpy as np
+
+VOCAB_SIZE = 256
+SOS_TOKEN = 256
+PRETRAINED_DIR = Path(__file__).resolve().parent / "pretrained"
+DEFAULT_QUANT_LOSSLESS_MODEL_PATH = str(PRETRAINED_DIR / "lossless.npz")
+DEFAULT_QUANT_LOSSY_MODEL_PATH = str(PRETRAINED_DIR / "lossy.npz")
+DEFAULT_QUANT_MODEL_PATH = DEFAULT_QUANT_LOSSLESS_MODEL_PATH
+DEFAULT_LSB_SETTING_FOR_LOSSY_MODEL = 3
+
+
+@dataclass
+class IntLayer:
+    """One quantised linear layer: ``y = clamp(((x.W^T + b) * M0) >> shift)``."""
+
+    weight: np.ndarray          # int8 [N, K] (nn.Linear layout)
+    bias: np.ndarray            # int32 [N]
+    m0: np.ndarray              # int64 [N]  (per-tensor checkpoints repeat one value)
+    shift: np.ndarray           # int32 [N]
+    relu: bool
+
+    @property
+    def n(self) -> int:
+        return int(self.weight.shape[0])
+
+    @property
+    def k(self) -> int:
+        return int(self.weight.shape[1])
+
+
+@dataclass
+class IntModel:
+    emb: np.ndarray             # int8 [257, 128]
+    layers: list
+    window: int = 64
+    output_scale: float = 1.0
+    input_scale: float = 1.0
+    exp_lut: np.ndarray = field(default_factory=lambda: np.zeros(VOCAB_SIZE, np.int64))
+
+    @property
+    def macs_per_row(self) -> int:
+        return sum(layer.n * layer.k for layer in self.layers)
+
+
+def float_to_multiplier_shift(multiplier: float):
+    """``cpu_int_inference.py:17-21``: frexp significand scaled to Q31."""
+    if multiplier == 0:
+        return 0, 0
+    significand, exponent = math.frexp(multiplier)
+    return int(round(significand * (2 ** 31))), 31 - exponent
+
+
+def build_integer_exp_lut(output_scale, lut_precision_bits=38):
+    """``cpu_entropy_coding.py:49-61``: ``LUT[i] = max(int(exp(-i*s) * 2**38), 0)``.
+
+    Evaluated in decimal arithmetic at 50 significant digits on
+    ``Decimal(str(float(s)))``; ``int`` truncates toward zero.
+    """
+    scale = float(output_scale)
+    if not math.isfinite(scale) or scale < 0:
+        raise ValueError("output_scale must be a finite nonnegative number")
+    if not isinstance(lut_precision_bits, int) or not 0 <= lut_precision_bits <= 38:
+        raise ValueError("lut_precision_bits must be an integer in [0, 38]")
+    with localcontext() as ctx:
+        ctx.prec = 50
+        s = Decimal(str(scale))
+        one = Decimal(1 << lut_precision_bits)
+        values = [max(int((Decimal(-i) * s).exp() * one), 0) for i in range(VOCAB_SIZE)]
+    return np.asarray(values, dtype=np.int64)
+
+
+def _per_channel(value, n, dtype):
+    arr = np.asarray(value, dtype=dtype)
+    if arr.ndim == 0:
+        arr = np.full(n, arr, dtype=dtype)
+    if arr.shape != (n,):
+        raise ValueError("per-channel requant parameters must have one value per output")
+    return np.ascontiguousarray(arr)
+
+
+def make_layer(weight, bias, m0, shift, relu) -> IntLayer:
+    weight = np.ascontiguousarray(np.asarray(weight, dtype=np.int8))
+    if weight.ndim != 2 or min(weight.shape) < 1:
+        raise ValueError("weight must be a nonempty two-dimensional int8 array")
+    n = weight.shape[0]
+    bias = _per_channel(bias, n, np.int32)
+    m0 = _per_channel(m0, n, np.int64)
+    shift = _per_channel(shift, n, np.int32)
+    if np.any(m0 < 0) or np.any(m0 > (1 << 31)):
+        raise ValueError("The quantized multiplier must be in [0, 2**31]")
+    if np.any(shift < 0) or np.any(shift > 63):
+        raise ValueError("The quantized right shift must be in [0, 63]")
+    return IntLayer(weight, bias, m0, shift, bool(relu))
+
+
+def _from_pth(path, dim, num_dec_layers, window_size) -> IntModel:
+    """Restates ``load_cpu_decoder`` (``cpu_int_inference.py:395-445``) and
+    ``_extract_linear`` (``:350-368``) on a state dict read as data."""
+    import torch
+
+    state = torch.load(Path(path), map_location="cpu", weights_only=True)
+    try:
+        embedding = state["decoder.embedding_linear.weight"]
+        input_scale = float(state["decoder.quant.scale"].item())
+        if tuple(embedding.shape) != (257, dim // 2):
+            raise ValueError("Checkpoint embedding shape does not match --dim")
+        if not math.isfinite(input_scale) or input_scale <= 0:
+            raise ValueError("Invalid embedding quantization scale")
+        emb = torch.round(embedding / input_scale).clamp(-128, 127).to(torch.int8).numpy()
+        layers = []
+        s_in = input_scale
+        expected_input = (dim // 2) * window_size
+        for index in range(num_dec_layers + 1):
+            prefix = f"decoder.mlp.{index * 2}"
+            weight, bias = state[f"{prefix}._packed_params._packed_params"]
+            output_scale = float(state[f"{prefix}.scale"].item())
+            output_width = dim * 2 if index < num_dec_layers else VOCAB_SIZE
+            if tuple(weight.shape) != (output_width, expected_input):
+                raise ValueError(f"Checkpoint {prefix} shape does not match the architecture")
+            if not math.isfinite(output_scale) or output_scale <= 0:
+                raise ValueError(f"Invalid quantization scale for {prefix}")
+            if weight.dtype != torch.qint8 or weight.qscheme() not in (
+                    torch.per_tensor_affine, torch.per_tensor_symmetric):
+                raise ValueError("Expected per-tensor quantized int8 linear weights")
+            bias_scale = s_in * weight.q_scale()
+            if bias is None:
+                bias_q = np.zeros(output_width, dtype=np.int32)
+            else:
+                bias_q = torch.round(bias.detach().cpu() / bias_scale).to(torch.int32).numpy()
+            m0, shift = float_to_multiplier_shift(bias_scale / output_scale)
+            layers.append(make_layer(weight.int_repr().numpy(), bias_q, m0, shift,
+                                     index < num_dec_layers))
+            s_in = output_scale
+            expected_input = output_width
+        n_packed = sum(k.startswith("decoder.mlp.") and k.endswith("._packed_params._packed_params")
+                       for k in state)
+        if n_packed != num_dec_layers + 1:
+            raise ValueError("Checkpoint layer count does not match --num-dec-layers")
+    except KeyError as exc:
+        raise ValueError(f"Incomplete or incompatible quantized MLP checkpoint: {exc}") from exc
+    # output_scale buffer is float32 in both reference decoders
+    # (cpu_int_inference.py:444, quant_mlp_export.py:198).
+    out_scale = float(np.float32(s_in))
+    return IntModel(emb=np.ascontiguousarray(emb), layers=layers, window=window_size,
+                    output_scale=out_scale, input_scale=input_scale,
+                    exp_lut=build_integer_exp_lut(out_scale))
+
+
+def export_npz(model: IntModel, path) -> None:
+    """Write the integer model as an ``.npz`` (no pickles)."""
+    arrays = {
+        "emb": model.emb,
+        "window": np.int64(model.window),
+        "output_scale": np.float64(model.output_scale),
+        "input_scale": np.float64(model.input_scale),
+        "exp_lut": model.exp_lut,
+        "n_layers": np.int64(len(model.layers)),
+    }
+    for i, layer in enumerate(model.layers):
+        arrays[f"w{i}"] = layer.weight
+        arrays[f"b{i}"] = layer.bias
+        arrays[f"m0_{i}"] = layer.m0
+        arrays[f"shift{i}"] = layer.shift
+        arrays[f"relu{i}"] = np.int64(layer.relu)
+    np.savez_compressed(path, **arrays)
+
+
+def _from_npz(path, window_size) -> IntModel:
+    with np.load(path, allow_pickle=False) as z:
+        layers = [make_layer(z[f"w{i}"], z[f"b{i}"], z[f"m0_{i}"], z[f"shift{i}"],
+                             bool(z[f"relu{i}"])) for i in range(int(z["n_layers"]))]
+        model = IntModel(emb=np.ascontiguousarray(z["emb"]), layers=layers,
+                         window=int(z["window"]), output_scale=float(z["output_scale"]),
+                         input_scale=float(z["input_scale"]),
+                         exp_lut=np.ascontiguousarray(z["exp_lut"]))
+    if window_size is not None and int(window_size) != model.window:
+        raise ValueError("Model window size does not match --window-size")
+    return model
+
+
+def load_int_model(model_path=None, dim=None, num_dec_layers=None, window_size=None) -> IntModel:
+    """Load a checkpoint (``.pth`` PTQ state dict or ``.npz`` integer export)."""
+    path = Path(model_path or DEFAULT_QUANT_MODEL_PATH)
+    dim = 256 if dim is None else int(dim)
+    num_dec_layers = 8 if num_dec_layers is None else int(num_dec_layers)
+    if dim < 2 or num_dec_layers < 0 or (window_size is not None and int(window_size) < 1):
+        raise ValueError("Invalid MLP architecture")
+    if path.suffix == ".npz":
+        model = _from_npz(path, window_size)
+    else:
+        model = _from_pth(path, dim, num_dec_layers, 64 if window_size is None else int(window_size))
+    validate_model(model)
+    return model
+
+
+def validate_model(model: IntModel) -> None:
+    if model.emb.dtype != np.int8 or model.emb.ndim != 2 or model.emb.shape[0] != SOS_TOKEN + 1:
+        raise ValueError("embedding must be int8 [257, dim/2]")
+    width = model.window * model.emb.shape[1]
+    for layer in model.layers:
+        if layer.k != width:
+            raise ValueError("layer input width does not match the previous layer")
+        width = layer.n
+    if width != VOCAB_SIZE:
+        raise ValueError("last layer must produce 256 logits")
+    lut = np.asarray(model.exp_lut)
+    if lut.shape != (VOCAB_SIZE,) or lut[0] <= 0 or np.any(lut < 0) or np.any(lut > (1 << 38)):
+        raise ValueError("exp_lut must be nonnegative, at most 2**38, and start positive")
+
+
+def random_int_model(seed=0, window=64, emb_dim=128, hidden=512, n_hidden=8,
+                     per_channel=True) -> IntModel:
+    """Seeded random integer model with the bundled checkpoints' layer dims.
+
+    Weights are uniform int8 in [-127, 127], biases int32, and the requant
+    multiplier/shift are drawn per output channel so that activations keep a
+    spread instead of saturating (the MLP microbenchmark's weights).
+    """
+    rng = np.random.Generator(np.random.PCG64(seed))
+    emb = rng.integers(-127, 128, size=(SOS_TOKEN + 1, emb_dim), dtype=np.int8)
+    dims = [window * emb_dim] + [hidden] * n_hidden + [VOCAB_SIZE]
+    layers = []
+    for i in range(len(dims) - 1):
+        k, n = dims[i], dims[i + 1]
+        w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        b = rng.integers(-20000, 20000, size=n, dtype=np.int32)
+        # accumulators have std ~ 73*73*sqrt(k); map that to ~40 output units
+        target = 40.0 / (73.0 * 73.0 * math.sqrt(k) * (0.6 if i else 1.0))
+        scales = target * rng.uniform(0.5, 2.0, size=n)
+        if not per_channel:
+            scales[:] = scales[0]
+        ms = [float_to_multiplier_shift(float(s)) for s in scales]
+        layers.append(make_layer(w, b, [m for m, _ in ms], [s for _, s in ms], i < len(dims) - 2))
+    out_scale = 0.05
+    return IntModel(emb=emb, layers=layers, window=window, output_scale=out_scale,
+                    input_scale=1.0, exp_lut=build_integer_exp_lut(out_scale))

@@ -1,0 +1,255 @@
+"""Write the golden fixtures in tests/golden from the reference implementation.
+
+Run in the build container only (the reference is not present on the GPU
+box):  ``python tests/golden/make_golden.py [/root/reference]``.
+
+The reference's own CPU backend is imported as a library and driven with
+its pure-Python / numpy backends (numba is absent here):
+
+* ``cpu_int_inference.load_cpu_decoder`` + ``CPUBitExactMLPDecoder._ar_step``
+  (``backend='int_mm'`` cross-checked against ``backend='numpy'``, torch
+  epilogue) -> int8 logits for seeded context windows on both checkpoints;
+* ``cpu_entropy_coding.build_integer_exp_lut`` / ``int8_logits_to_cdf``;
+* ``CpuRangeStepEncoder`` / ``CpuRangeDecoder`` with ``backend='python'``
+  -> exact u32 word streams and decoded symbols;
+* ``cpu_compression.ReadFramingMixin.batch_inference_reads`` around a
+  ``compress_chunks`` / ``decompress_chunks`` pair composed of the functions
+  above exactly as ``CPUQuantMLPCompression`` composes them
+  (``cpu_compression.py:178-332``; that class itself requires numba)
+  -> framed per-read payload bytes for seeded synthetic reads.
+
+Only inputs and outputs are written (``.npz`` without pickles, JSON).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parents[1]
+sys.path.insert(0, str(REPO))
+
+from sigcomp_amd import signal, synth  # noqa: E402
+
+SOS = 256
+WINDOW = 64
+
+
+def _sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def _contexts(rng, n, token_pool=None):
+    """Seeded windows: all-SOS, SOS-padded prefixes, realistic and extreme tokens."""
+    ctx = np.full((n, WINDOW), SOS, dtype=np.int64)
+    for i in range(n):
+        kind = i % 6
+        if kind == 0 and i == 0:
+            continue  # all SOS (first step of every chunk)
+        if kind in (0, 1):  # SOS-padded prefix of a real sequence
+            keep = int(rng.integers(1, WINDOW))
+            src = token_pool[rng.integers(0, len(token_pool) - keep):][:keep]
+            ctx[i, WINDOW - keep:] = src
+        elif kind == 2:  # realistic full window
+            start = int(rng.integers(0, len(token_pool) - WINDOW))
+            ctx[i] = token_pool[start:start + WINDOW]
+        elif kind == 3:  # uniform tokens
+            ctx[i] = rng.integers(0, 256, WINDOW)
+        elif kind == 4:  # extremes
+            ctx[i] = rng.choice(np.array([0, 1, 254, 255, 256]), WINDOW)
+        else:  # constant token
+            ctx[i] = int(rng.integers(0, 257))
+    return ctx
+
+
+def main(ref_root="/root/reference"):
+    sys.path.insert(0, str(ref_root))
+    from sigcomp import cpu_entropy_coding as ce
+    from sigcomp import cpu_int_inference as ci
+    from sigcomp.cpu_compression import ReadFramingMixin
+
+    rng = np.random.Generator(np.random.PCG64(20261201))
+    pool = np.concatenate([signal.split_signal(r)[1]
+                           for r in synth.synth_reads(8, 11, synth.DNA)]).astype(np.int64)
+    constants = {}
+    models = {}
+    for name in ("lossless", "lossy"):
+        path = Path(ref_root) / "sigcomp" / "pretrained_models" / f"{name}.pth"
+        dec = ci.load_cpu_decoder(path, backend="int_mm", epilogue="torch")
+        dec_np = ci.load_cpu_decoder(path, backend="numpy", epilogue="torch")
+        lut = ce.build_integer_exp_lut(float(dec.output_scale))
+        models[name] = (dec, lut)
+        layers = []
+        for layer in dec.mlp:
+            layers.append({
+                "m0": int(layer.M0), "shift": int(layer.shift), "relu": bool(layer.has_relu),
+                "weight_sha256": _sha(layer.weight_q.numpy()),
+                "bias_sha256": _sha(layer.bias_q.numpy()),
+                "bias_min": int(layer.bias_q.min()), "bias_max": int(layer.bias_q.max()),
+            })
+        constants[name] = {
+            "output_scale": float(dec.output_scale),
+            "emb_sha256": _sha(dec.embedding.weight_q.numpy()),
+            "layers": layers,
+            "exp_lut": [int(v) for v in lut],
+        }
+        # MLP logits on seeded windows
+        ctx = _contexts(rng, 192, pool)
+        with torch.no_grad():
+            logits = dec._ar_step(torch.from_numpy(ctx))[:, 0].numpy().copy()
+            logits_np = dec_np._ar_step(torch.from_numpy(ctx))[:, 0].numpy()
+        assert np.array_equal(logits, logits_np), "reference backends disagree"
+        # logits -> CDF: model logits + crafted rows
+        crafted = [np.zeros(256, np.int8), np.full(256, 127, np.int8), np.full(256, -128, np.int8)]
+        one = np.full(256, -128, np.int8); one[17] = 127; crafted.append(one)
+        two = np.zeros(256, np.int8); two[3] = 90; two[200] = 90; crafted.append(two)
+        crafted.append(np.arange(256).astype(np.int8))
+        crafted.extend(rng.integers(-128, 128, (26, 256)).astype(np.int8))
+        cdf_in = np.concatenate([logits, np.stack(crafted)])
+        cdf = ce.int8_logits_to_cdf(cdf_in, lut)
+        np.savez_compressed(HERE / f"mlp_{name}.npz", ctx=ctx, logits=logits)
+        np.savez_compressed(HERE / f"cdf_{name}.npz", logits=cdf_in, cdf=cdf)
+    (HERE / "constants.json").write_text(json.dumps(constants, indent=1) + "\n")
+
+    # Range coder streams (python backend), several logit regimes and lengths.
+    streams = []
+    for name in ("lossless", "lossy"):
+        dec, lut = models[name]
+        for kind, length in (("uniform", 300), ("realistic", 700), ("peaky_tail", 200),
+                             ("argmax", 150), ("equal", 64), ("mixed", 1)):
+            if kind == "realistic":
+                start = int(rng.integers(0, len(pool) - length))
+                sym = pool[start:start + length].copy()
+                ctx = np.full((length, WINDOW), SOS, np.int64)
+                full = np.concatenate([np.full(WINDOW, SOS, np.int64), sym])
+                for t in range(length):
+                    ctx[t] = full[t:t + WINDOW]
+                with torch.no_grad():
+                    lg = dec._ar_step(torch.from_numpy(ctx))[:, 0].numpy().copy()
+            elif kind == "uniform":
+                lg = rng.integers(-128, 128, (length, 256)).astype(np.int8)
+                sym = rng.integers(0, 256, length)
+            elif kind == "peaky_tail":
+                lg = np.full((length, 256), -100, np.int8)
+                hot = rng.integers(0, 256, length)
+                lg[np.arange(length), hot] = 120
+                sym = (hot + rng.integers(1, 256, length)) % 256
+            elif kind == "argmax":
+                lg = rng.integers(-30, 30, (length, 256)).astype(np.int8)
+                sym = lg.astype(np.int16).argmax(axis=1)
+            elif kind == "equal":
+                lg = np.zeros((length, 256), np.int8)
+                sym = rng.integers(0, 256, length)
+            else:
+                lg = rng.integers(-128, 128, (length, 256)).astype(np.int8)
+                sym = rng.integers(0, 256, length)
+            streams.append((name, kind, lg, sym.astype(np.int64), lut))
+
+    # Encode all streams of one model as one batch (exercises valid_lens).
+    out = {}
+    for name in ("lossless", "lossy"):
+        group = [s for s in streams if s[0] == name]
+        lut = group[0][4]
+        B = len(group)
+        T = max(len(s[3]) for s in group)
+        lg = np.zeros((B, T, 256), np.int8)
+        sy = np.zeros((B, T), np.int64)
+        valid = np.array([len(s[3]) for s in group], np.int64)
+        for b, s in enumerate(group):
+            lg[b, :len(s[3])] = s[2]
+            sy[b, :len(s[3])] = s[3]
+        enc = ce.CpuRangeStepEncoder(B, T + 32, backend="python")
+        enc.encode_logits(lg, lut, sy, valid, t_start=0)
+        words = enc.get_compressed()
+        decd = ce.CpuRangeDecoder(words, backend="python")
+        got = np.zeros((B, T), np.int64)
+        for t in range(T):
+            got[:, t] = decd.decode_step_int8(lg[:, t], lut, valid, t)
+        for b, s in enumerate(group):
+            assert np.array_equal(got[b, :valid[b]], s[3]), "reference round trip failed"
+            key = f"{name}_{s[1]}"
+            out[f"{key}_logits"] = s[2]
+            out[f"{key}_symbols"] = s[3]
+            out[f"{key}_words"] = np.frombuffer(words[b], dtype="<u4").astype(np.uint32)
+            out[f"{key}_decoded"] = got[b, :valid[b]]
+        # step-API variant: one encode_step_int8 call per t must give the same words
+        enc2 = ce.CpuRangeStepEncoder(B, T + 32, backend="python")
+        for t in range(T):
+            enc2.encode_step_int8(lg[:, t], lut, sy[:, t], valid, t)
+        assert enc2.get_compressed() == words
+    np.savez_compressed(HERE / "coder_streams.npz", **out)
+
+    # End-to-end: framed per-read payloads (s_bytes) for seeded synthetic reads.
+    class Harness(ReadFramingMixin):
+        def __init__(self, dec, lut, chunk_len):
+            self.dec, self.lut, self.chunk_len = dec, lut, chunk_len
+
+        def compress_chunks(self, chunks, max_batch_size=64, use_perfect=False, use_tqdm=False):
+            res = []
+            for s0 in range(0, len(chunks), max_batch_size):
+                batch = [np.asarray(c, np.uint8) for c in chunks[s0:s0 + max_batch_size]]
+                valid = np.array([len(c) for c in batch], np.int64)
+                size, max_len = len(batch), int(valid.max())
+                context = np.full((size, WINDOW + max_len), SOS, np.int64)
+                symbols = context[:, WINDOW:]
+                symbols.fill(0)
+                for b, c in enumerate(batch):
+                    symbols[b, :len(c)] = c
+                windows = np.lib.stride_tricks.sliding_window_view(context, WINDOW, axis=1)
+                with torch.no_grad():
+                    lg = self.dec._ar_step(torch.from_numpy(
+                        np.ascontiguousarray(windows[:, :max_len]).reshape(-1, WINDOW)))
+                lg = lg.reshape(size, max_len, 256).numpy()
+                enc = ce.CpuRangeStepEncoder(size, self.chunk_len + 32, backend="python")
+                enc.encode_logits(lg, self.lut, symbols[:, :max_len], valid, t_start=0)
+                res.extend(enc.get_compressed())
+            return res
+
+        def decompress_chunks(self, chunk_bytes, valid_lengths, max_batch_size=64,
+                              use_perfect=False, use_tqdm=False):
+            res = []
+            for s0 in range(0, len(chunk_bytes), max_batch_size):
+                batch = chunk_bytes[s0:s0 + max_batch_size]
+                valid = np.asarray(valid_lengths[s0:s0 + max_batch_size], np.int64)
+                size, max_len = len(batch), int(valid.max())
+                decd = ce.CpuRangeDecoder(batch, backend="python")
+                context = np.full((size, WINDOW + max_len), SOS, np.int64)
+                for t in range(max_len):
+                    with torch.no_grad():
+                        lg = self.dec._ar_step(torch.from_numpy(
+                            np.ascontiguousarray(context[:, t:t + WINDOW])))
+                    context[:, t + WINDOW] = decd.decode_step_int8(lg[:, 0].numpy(), self.lut,
+                                                                   valid, t)
+                res.extend(context[b, WINDOW:WINDOW + n].astype(np.uint8)
+                           for b, n in enumerate(valid))
+            return res
+
+    e2e = {}
+    for name, lsb, profile, lengths in (("lossless", 0, synth.DNA, [2, 40, 900, 2300, 4200]),
+                                        ("lossy", 3, synth.RNA, [3, 700, 2500])):
+        dec, lut = models[name]
+        reads = synth.synth_reads(len(lengths), 4242 + lsb, profile, lengths=lengths)
+        small = [signal.split_signal(signal.prepare_signal(r, lsb))[1] for r in reads]
+        h = Harness(dec, lut, chunk_len=2048)
+        framed = h.batch_inference_reads(list_of_reads=small, batch_size=3)
+        back = h.batch_inference_reads(list_of_compressed_reads=framed,
+                                       list_of_lengths=[len(s) for s in small], batch_size=4)
+        for s, b in zip(small, back):
+            assert np.array_equal(s, b), "reference e2e round trip failed"
+        for i, (r, f) in enumerate(zip(reads, framed)):
+            e2e[f"{name}_read{i}_signal"] = r
+            e2e[f"{name}_read{i}_sbytes"] = np.frombuffer(f, dtype=np.uint8)
+        e2e[f"{name}_lsb"] = np.int64(lsb)
+        e2e[f"{name}_nreads"] = np.int64(len(reads))
+    np.savez_compressed(HERE / "e2e_reads.npz", **e2e)
+    print("golden fixtures written to", HERE)
+
+
+if __name__ == "__main__":
+    main(*sys.argv[1:])
