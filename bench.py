@@ -1,0 +1,269 @@
+"""SigComp codec benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c2]
+
+Default workload (config c3+c4): 4,000 seeded synthetic R10.4.1-like reads
+(~80 M int16 samples), bundled lossless model, chunk_len 2048.  One step =
+one GPU compress of every chunk (teacher-forced MLP fused with the frequency
+step, then range encoder) followed by the GPU decompress of the resulting
+streams (persistent autoregressive decode of all chunks at once).  Inputs
+(token chunks / range-coded words) are resident in HBM before the timed
+region; host-side signal split and framing are outside it.
+
+Prints one JSON line: value = round-trip Msamples/s (samples / (compress +
+decompress time)); compress and decompress rates, bits/sample, the
+roofline of the dominant kernel (k_decompress, int8 MFMA bound) measured
+with HIP events on its own stream, and the CPU oracle baseline on a bounded
+sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c2 = MLP
+microbenchmark (1,048,576 context rows -> int32 CDF tables).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+OPS_PER_ROW = 2 * (8192 * 512 + 7 * 512 * 512 + 512 * 256)   # 12,320,768 int8 ops
+PEAK_INT8_TOPS = 5000.0                                       # MI355X dense int8
+PEAK_HBM_GBS = 8000.0
+CHUNK_LEN = 2048
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_workload(cfg_name, n_reads):
+    from sigcomp_amd import signal, synth
+    cfg = synth.CONFIGS[cfg_name]
+    reads = synth.synth_reads(n_reads or cfg["n_reads"], cfg["seed"], cfg["profile"])
+    samples = int(sum(len(r) for r in reads))
+    small = [signal.split_signal(signal.prepare_signal(r, cfg["lsb"]))[1] for r in reads]
+    chunks = [s[i:i + CHUNK_LEN] for s in small for i in range(0, len(s), CHUNK_LEN)]
+    return cfg, reads, samples, small, chunks
+
+
+def bench_codec(args):
+    import torch
+    from sigcomp_amd import _hip
+    from sigcomp_amd.model_io import DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+
+    cfg, reads, samples, small, chunks = build_workload(args.config, args.n_reads)
+    model_path = DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy" else DEFAULT_QUANT_LOSSLESS_MODEL_PATH
+    codec = QuantMLPCompression(chunk_len=CHUNK_LEN, gpu=0, model_path=model_path)
+    n = len(chunks)
+    lengths = np.array([len(c) for c in chunks], np.int32)
+    n_tokens = int(lengths.sum())
+    log(f"[bench] {args.config}: {len(reads)} reads, {samples} samples, {n_tokens} tokens, {n} chunks")
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(lengths[:-1], out=tok_off[1:])
+    cap = (lengths + 2).astype(np.int32)
+    word_off = np.zeros(n, np.int64)
+    np.cumsum(cap[:-1].astype(np.int64), out=word_off[1:])
+    dev = torch.device("cuda:0")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    t_tokens, t_tok_off, t_len, t_word_off, t_cap = d(np.concatenate(chunks)), d(tok_off), d(lengths), d(word_off), d(cap)
+    words, cnt, status, ws = codec._compress_buffers(n, n_tokens, int(cap.sum()))
+    order = np.argsort(-lengths, kind="stable")
+    o_woff, o_len, o_toff = d(word_off[order]), d(lengths[order]), d(tok_off[order])
+    o_idx = d(order.astype(np.int64))
+    o_cnt = torch.empty(n, dtype=torch.int32, device=dev)
+    out_tokens = torch.empty(n_tokens, dtype=torch.uint8, device=dev)
+    dstatus = torch.empty(n, dtype=torch.int32, device=dev)
+    L = _hip.lib()
+    stream = torch.cuda.Stream(device=dev)          # default priority
+    h = codec.hip.handle
+
+    def compress():
+        _hip.check(L.sc_compress_chunks(h, _hip.ptr(t_tokens), _hip.ptr(t_tok_off), _hip.ptr(t_len), n,
+                                        n_tokens, _hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(t_cap),
+                                        _hip.ptr(cnt), _hip.ptr(status), _hip.ptr(ws), ws.numel(),
+                                        stream.cuda_stream))
+
+    def decompress():
+        torch.index_select(cnt, 0, o_idx, out=o_cnt)
+        _hip.check(L.sc_decompress_chunks(h, _hip.ptr(words), _hip.ptr(o_woff), _hip.ptr(o_cnt),
+                                          _hip.ptr(o_len), n, _hip.ptr(out_tokens), _hip.ptr(o_toff),
+                                          _hip.ptr(dstatus), stream.cuda_stream))
+
+    with torch.cuda.device(dev), torch.cuda.stream(stream):
+        for w in range(args.warmup):
+            compress(); decompress()
+            stream.synchronize()
+            log(f"[bench] warmup {w + 1}/{args.warmup} done")
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(args.steps):
+            ev[k][0].record(stream)
+            compress()
+            ev[k][1].record(stream)
+            decompress()
+            ev[k][2].record(stream)
+        stream.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    t_c = np.mean([e[0].elapsed_time(e[1]) for e in ev]) / 1e3
+    t_d = np.mean([e[1].elapsed_time(e[2]) for e in ev]) / 1e3
+    if int(status.sum().item()) or int(dstatus.sum().item()):
+        raise RuntimeError("codec reported a stream error")
+    # parity: lossless round trip on every chunk; chunk bytes vs the CPU oracle on a sample
+    back = out_tokens.cpu().numpy()
+    if not np.array_equal(back, t_tokens.cpu().numpy()):
+        raise RuntimeError("round trip mismatch")
+    cnt_np = cnt.cpu().numpy()
+    words_np = words.cpu().numpy().view(np.uint32)
+    comp_bytes = int(cnt_np.sum()) * 4 + 2 * n
+    parity = oracle_sample_check(codec.model, chunks, words_np, word_off, cnt_np)
+    log(f"[bench] compress {t_c * 1e3:.1f} ms, decompress {t_d * 1e3:.1f} ms, oracle sample ok={parity}")
+    rows = n_tokens
+    achieved = rows * OPS_PER_ROW / t_d / 1e12
+    res = {
+        "metric": "compress/decompress Msamples/s on 1 MI355X; INT8 MFMA util; archive bits/sample",
+        "value": round(samples / (t_c + t_d) / 1e6, 3),
+        "unit": "Msamples/s (round trip)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round((t_c + t_d) * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {len(reads)} reads, {samples} samples, {n} chunks of "
+                               f"<= {CHUNK_LEN} tokens, model {cfg['model']}, lsb {cfg['lsb']}",
+                   "reads": len(reads), "samples": samples, "tokens": n_tokens, "chunks": n},
+        "compress_msamples_s": round(samples / t_c / 1e6, 3),
+        "decompress_msamples_s": round(samples / t_d / 1e6, 3),
+        "bits_per_sample_tokens": round(comp_bytes * 8 / samples, 4),
+        "parity": {"round_trip": True, "oracle_sample_chunks": parity},
+        "wall_s_timed": round(wall, 3),
+        "roofline": {"kernel": "k_decompress", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                     "traffic": None,
+                     "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch"},
+    }
+    return res, chunks, samples, cfg
+
+
+def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    rng = np.random.default_rng(0)
+    idx = np.sort(rng.choice(len(chunks), size=min(k, len(chunks)), replace=False))
+    ref = oracle.compress_chunks(oracle.OracleModel(model), [chunks[i] for i in idx])
+    for j, i in enumerate(idx):
+        got = words_np[word_off[i]:word_off[i] + cnt_np[i]].tobytes()
+        if got != ref[j]:
+            raise RuntimeError(f"chunk {i} differs from the CPU oracle")
+    return int(len(idx))
+
+
+def cpu_baseline(model, chunks, samples_per_token, budget_s=20.0):
+    """CPU oracle (C restatement of the reference CPU backend) on a bounded
+    sample of the same chunks: compress then decompress, all host threads."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    threads = oracle.cpu_count()
+    oracle.set_num_threads(threads)
+    om = oracle.OracleModel(model)
+    rng = np.random.default_rng(1)
+    # calibrate with a few chunks, then size the sample to the budget
+    pick = list(rng.choice(len(chunks), size=min(len(chunks), 2 * threads), replace=False))
+    sample = [chunks[i] for i in pick]
+    t0 = time.perf_counter()
+    comp = oracle.compress_chunks(om, sample)
+    tc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    oracle.decompress_chunks(om, comp, [len(c) for c in sample])
+    td = time.perf_counter() - t0
+    toks = sum(len(c) for c in sample)
+    sm = toks * samples_per_token
+    return {"value": round(sm / (tc + td) / 1e6, 5), "unit": "Msamples/s (round trip)",
+            "cores": threads, "kind": "port",
+            "compress_msamples_s": round(sm / tc / 1e6, 5),
+            "decompress_msamples_s": round(sm / td / 1e6, 5),
+            "sample": f"{len(sample)} random chunks ({toks} tokens) of the same workload, "
+                      f"compress + decompress with the C oracle on {threads} threads"}
+
+
+def bench_mlp(args):
+    """Config c2: 1,048,576 context rows -> int32 CDF tables, seeded random
+    per-channel model with the bundled checkpoints' layer dims."""
+    import torch
+    from sigcomp_amd import signal, synth
+    from sigcomp_amd.model_io import random_int_model
+    from sigcomp_amd.quant_mlp_export import HipModel
+    rows = args.rows
+    m = random_int_model(seed=2, per_channel=True)
+    hm = HipModel(m, torch.device("cuda:0"))
+    toks = np.concatenate([signal.split_signal(r)[1] for r in synth.synth_reads(64, 202, synth.DNA)])
+    toks = toks.astype(np.int64)
+    starts = np.random.default_rng(3).integers(-63, len(toks) - 64, rows)
+    idx = starts[:, None] + np.arange(64)[None, :]
+    ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
+    ctx_d = torch.from_numpy(ctx).cuda()
+    for _ in range(args.warmup):
+        hm.forward_windows(ctx_d, "cdf")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        out = hm.forward_windows(ctx_d, "cdf")
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / args.steps
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    sub = np.random.default_rng(4).choice(rows, 256, replace=False)
+    om = oracle.OracleModel(m)
+    ref = oracle.logits_to_cdf(oracle.mlp_forward(om, ctx[sub]), m.exp_lut)
+    if not np.array_equal(out[torch.from_numpy(sub).cuda()].cpu().numpy().astype(np.int64), ref):
+        raise RuntimeError("c2 CDF mismatch vs oracle")
+    achieved = rows * OPS_PER_ROW / t / 1e12
+    return {"metric": "INT8 MLP rows/s -> int32 CDF (c2 microbench)", "value": round(rows / t / 1e6, 3),
+            "unit": "Mrows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(t * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": f"c2: {rows} context rows, random per-channel int8 model"},
+            "roofline": {"kernel": "k_mlp_context<cdf>", "bound": "mfma", "achieved": round(achieved, 2),
+                         "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2"])
+    ap.add_argument("--n-reads", type=int, default=None)
+    ap.add_argument("--rows", type=int, default=1 << 20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the codec shards by independent reads with no "
+              "collective, so multi-GPU runs are out of scope for this build", file=sys.stderr)
+        sys.exit(2)
+    if args.config == "c2":
+        print(json.dumps(bench_mlp(args)), flush=True)
+        return
+    res, chunks, samples, cfg = bench_codec(args)
+    if not args.no_cpu_baseline:
+        from sigcomp_amd.model_io import load_int_model, DEFAULT_QUANT_LOSSY_MODEL_PATH, DEFAULT_QUANT_LOSSLESS_MODEL_PATH
+        model = load_int_model(DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy"
+                               else DEFAULT_QUANT_LOSSLESS_MODEL_PATH)
+        log("[bench] cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline(model, chunks, samples / res["config"]["tokens"])
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

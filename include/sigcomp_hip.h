@@ -1,0 +1,186 @@
+/*
+ * sigcomp_hip.h -- C ABI of the MI355X (gfx950) SigComp codec library.
+ *
+ * libsigcomp_hip.so holds hand-written HIP kernels for the codec hot path of
+ * SigComp (BioinfoSZU/SigComp v1.1.0): the integer-quantised MLP entropy model
+ * on int8 MFMA with fused requantisation, the fused int8-logits -> frequency /
+ * CDF step, the range encoder and decoder, and the batched autoregressive
+ * decode loop.  Every entry point below names the reference interface it
+ * replaces (paths relative to the reference's sigcomp/ package).
+ *
+ * Conventions
+ *  - Pointers documented "device" are HIP device pointers owned by the caller
+ *    (the library never frees caller memory).  "host" pointers are read during
+ *    the call only.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
+ *    work is stream-ordered; no call synchronises the device.
+ *  - Return value: SC_OK or an SC_ERR_* code for argument / HIP errors found
+ *    at launch time; sc_last_error() describes the last failure of the calling
+ *    thread.  Data-dependent failures (an out-of-range token, an encoder
+ *    capacity overflow, an invalid range stream) are reported through the
+ *    caller's device `status` arrays with the SC_STATUS_* codes, since they
+ *    are known only after the kernels ran.
+ *  - One model handle may be used from several streams; calls that share a
+ *    workspace or state arrays must not overlap.
+ *
+ * Architecture supported by the kernels: window 64, embedding 257 x 128,
+ * layer 0 8192 -> 512, n_layers - 2 hidden layers 512 -> 512, last layer
+ * 512 -> 256 (the bundled lossless and lossy checkpoints,
+ * quant_mlp_export.py:211-213, cpu_int_inference.py:395-445).
+ */
+#ifndef SIGCOMP_HIP_H
+#define SIGCOMP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SC_OK 0
+#define SC_ERR_ARG 1
+#define SC_ERR_HIP 2
+#define SC_ERR_UNSUPPORTED 3
+
+/* Per-row / per-stream status codes written to device status arrays. */
+#define SC_STATUS_OK 0
+#define SC_STATUS_CAPACITY 1        /* encoder output capacity exceeded (OverflowError) */
+#define SC_STATUS_INVALID_STREAM 2  /* decoder: scale == 0 or quantile >= 2**24 (ValueError) */
+#define SC_STATUS_BAD_TOKEN 3       /* context token outside [0, 256] (ValueError) */
+
+#define SC_VOCAB 256
+#define SC_SOS 256
+
+typedef struct sc_model sc_model;
+
+/* One quantised linear layer, host arrays, nn.Linear layout.
+ * y = clamp(((x . W^T + bias) * m0) >> shift, relu ? 0 : -128, 127). */
+typedef struct {
+    int32_t n, k;
+    const int8_t *weight;   /* [n, k] */
+    const int32_t *bias;    /* [n]    */
+    const int64_t *m0;      /* [n], each in [0, 2**31] (per-tensor models repeat one value) */
+    const int32_t *shift;   /* [n], each in [0, 63] */
+    int32_t relu;
+} sc_layer_desc;
+
+/* Last error message of the calling thread (never NULL). */
+const char *sc_last_error(void);
+
+/* Library version string. */
+const char *sc_version(void);
+
+/* Upload an integer model to `device` and pack its weights in MFMA fragment
+ * order.  Replaces QuantMLPCompression.__init__ + convert_ptq_to_gpu_pipeline
+ * (quant_mlp_export.py:215-269,180-200) after the host has derived the
+ * integer constants (cpu_int_inference.py:395-445); `exp_lut` is the 256-entry
+ * integer exp table of build_integer_exp_lut (gpu_entropy_coding.py:8-22). */
+int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_t window,
+                    const sc_layer_desc *layers, int32_t n_layers, const int64_t *exp_lut,
+                    int32_t device, sc_model **out);
+int sc_model_destroy(sc_model *model);
+
+/* Device copy of the model's exp LUT (uint64 [256]); owned by the model. */
+const uint64_t *sc_model_lut(const sc_model *model);
+
+/* MLP forward on explicit context windows: ctx int64 [rows, 64] (device,
+ * tokens in [0, 256]) -> logits int8 [rows, 256] (device).  Replaces
+ * GPUBitExactMLPDecoder._ar_step (quant_mlp_export.py:133-138) = int8
+ * embedding gather + 9 x bit_exact_linear_kernel launches
+ * (quant_mlp_export.py:21-110).  status: device int32 [1], set to
+ * SC_STATUS_BAD_TOKEN if any token is out of range (never cleared). */
+int sc_mlp_forward(const sc_model *model, const int64_t *ctx, int64_t rows, int8_t *logits,
+                   int32_t *status, void *stream);
+
+/* MLP forward fused with the logits -> CDF step: ctx int64 [rows, 64] ->
+ * cdf int32 [rows, 257] (cdf[0] = 0, cdf[256] = 2**24).  Equals
+ * int8_logits_to_cdf(_ar_step(ctx)) (gpu_entropy_coding.py:25-51,
+ * cpu_entropy_coding.py:73-110) without materialising the logits. */
+int sc_mlp_forward_cdf(const sc_model *model, const int64_t *ctx, int64_t rows, int32_t *cdf,
+                       int32_t *status, void *stream);
+
+/* int8 logits [rows, 256] + LUT (device uint64/int64 [256]) -> int64 CDF
+ * [rows, 257].  Replaces int8_logits_to_cdf (gpu_entropy_coding.py:25-51). */
+int sc_logits_to_cdf(const int8_t *logits, int64_t rows, const uint64_t *lut, int64_t *cdf,
+                     void *stream);
+
+/* Range encoder state, one entry per stream (device arrays [B]).
+ * Mirrors GpuRangeStepEncoder's tensors (gpu_entropy_coding.py:255-267). */
+typedef struct {
+    uint64_t *lower;        /* init 0            */
+    uint64_t *range;        /* init 2**64 - 1    */
+    int32_t *inverted;      /* init 0            */
+    uint32_t *first;        /* init 0            */
+    int32_t *write_pos;     /* init 0            */
+    int32_t *status;        /* init 0            */
+} sc_encoder_state;
+
+/* One encoder step for every stream b with t < valid_lens[b]: frequencies
+ * from logits[b] (int8 [B, 256]) and the LUT, then the range-coder update
+ * with symbols[b] (int64 [B]); words go to words[b * max_words + pos].
+ * Replaces GpuRangeStepEncoder.encode_step_int8 / _range_encode_step_int8_kernel
+ * (gpu_entropy_coding.py:270-280,137-252). */
+int sc_encode_step(const int8_t *logits, const uint64_t *lut, const int64_t *symbols,
+                   const int64_t *valid_lens, int64_t t, int64_t B, const sc_encoder_state *state,
+                   uint32_t *words, int64_t max_words, void *stream);
+
+/* Flush every stream (GpuRangeStepEncoder.seal / _range_seal_kernel,
+ * gpu_entropy_coding.py:282-290,78-134).  Sealing twice emits nothing more. */
+int sc_encode_seal(int64_t B, const sc_encoder_state *state, uint32_t *words, int64_t max_words,
+                   void *stream);
+
+/* Range decoder state (device arrays [B]); mirrors GpuRangeDecoder's tensors
+ * (gpu_entropy_coding.py:400-442). */
+typedef struct {
+    uint64_t *lower;        /* init 0                                   */
+    uint64_t *range;        /* init 2**64 - 1                           */
+    uint64_t *point;        /* init: first two words, big word first    */
+    int64_t *read_pos;      /* index into words of the next word        */
+    const int64_t *end_pos; /* one past the stream's last word          */
+    int32_t *status;        /* init 0                                   */
+} sc_decoder_state;
+
+/* One decoder step: symbols_out[b] (int64 [B]) = decoded symbol, or 256 for
+ * streams with t >= valid_lens[b] or a failed stream.  Replaces
+ * GpuRangeDecoder.decode_step_int8 / _range_decode_step_int8_kernel
+ * (gpu_entropy_coding.py:444-454,306-397). */
+int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *valid_lens, int64_t t,
+                   int64_t B, const sc_decoder_state *state, const uint32_t *words,
+                   int64_t *symbols_out, void *stream);
+
+/* Bytes of device workspace sc_compress_chunks needs for n_tokens tokens. */
+int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks);
+
+/* Compress n_chunks independent token chunks (teacher-forced MLP over every
+ * step fused with the logits -> frequency step, then the range encoder and
+ * seal).  Chunk c: lengths[c] tokens (uint8) at tokens + tok_off[c]; its u32
+ * words go to words + word_off[c] (capacity word_cap[c] >= lengths[c] + 2 is
+ * always sufficient); word_cnt[c] and status[c] are written.  All arrays
+ * device.  Replaces QuantMLPCompression.compress_chunks /
+ * _compress_chunks_gpu_ar (quant_mlp_export.py:271-323) and produces the
+ * chunk bytes of CPUQuantMLPCompression.compress_chunks
+ * (cpu_compression.py:178-257). */
+int sc_compress_chunks(const sc_model *model, const uint8_t *tokens, const int64_t *tok_off,
+                       const int32_t *lengths, int64_t n_chunks, int64_t n_tokens,
+                       uint32_t *words, const int64_t *word_off, const int32_t *word_cap,
+                       int32_t *word_cnt, int32_t *status, void *workspace,
+                       int64_t workspace_bytes, void *stream);
+
+/* Decompress n_chunks chunks with one persistent kernel: every workgroup owns
+ * a tile of chunks and runs the whole autoregressive loop for them (MLP step,
+ * fused frequency step and decoder step per token, context kept on chip).
+ * Chunk c: word_cnt[c] words at words + word_off[c] -> lengths[c] tokens at
+ * tokens + tok_off[c]; status[c] is written (SC_STATUS_INVALID_STREAM on a
+ * corrupt stream).  All arrays device.  Replaces
+ * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
+ * (quant_mlp_export.py:325-377); output equals
+ * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */
+int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int64_t *word_off,
+                         const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,
+                         uint8_t *tokens, const int64_t *tok_off, int32_t *status, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIGCOMP_HIP_H */

@@ -65,7 +65,7 @@ class _Model(ctypes.Structure):
 
 def build() -> Path:
     """Compile the oracle with its Makefile (no-op when up to date)."""
-    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    subprocess.run(["make", "-s", "-B", "-C", str(HERE)], check=True)
     return LIB_PATH
 
 

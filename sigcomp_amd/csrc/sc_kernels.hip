@@ -1,0 +1,728 @@
+// sc_kernels.hip -- gfx950 kernels of the SigComp codec and their C ABI.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/sigcomp_hip.h"
+#include "sc_device.h"
+
+using namespace sc;
+
+// =========================================================================
+// Kernels
+// =========================================================================
+
+namespace {
+
+constexpr int RT_TILE = 4;          // rows per MLP tile = 32 * RT_TILE = 128
+constexpr int R_TILE = 32 * RT_TILE;
+constexpr int DEC_RT_MAX = 4;       // decode: up to 128 chunks per workgroup
+
+// ---- explicit context windows (GPUBitExactMLPDecoder._ar_step) ----------
+
+enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
+
+template <int MODE>
+__global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const int64_t *__restrict__ ctx,
+                                                            int64_t rows, int8_t *__restrict__ logits,
+                                                            int32_t *__restrict__ cdf,
+                                                            int32_t *__restrict__ status) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
+    __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
+    __shared__ uint64_t s_lut[VOCAB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
+    for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int64_t row0 = tile * R_TILE;
+        __syncthreads();
+        int bad = 0;
+        for (int i = threadIdx.x; i < R_TILE * WIN; i += THREADS) {
+            const int64_t row = row0 + i / WIN;
+            int64_t v = 0;
+            if (row < rows) {
+                v = ctx[row * WIN + (i % WIN)];
+                if (v < 0 || v > SOS) { bad = 1; v = 0; }
+            }
+            s_ctx[i] = (uint16_t)v;
+        }
+        if (bad) status[0] = SC_STATUS_BAD_TOKEN;
+        __syncthreads();
+        mlp_rows<RT_TILE, 2>(M, s_emb, s_act, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+                          wave, lane);
+        if (MODE == OUT_LOGITS) {
+            // 128 rows x 256 bytes, 16-byte chunks, coalesced
+            for (int i = threadIdx.x; i < R_TILE * 16; i += THREADS) {
+                const int r = i >> 4, c = i & 15;
+                if (row0 + r < rows)
+                    *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_off(r, c));
+            }
+        } else {
+            for (int r = wave; r < R_TILE; r += WAVES) {
+                if (row0 + r >= rows) break;
+                const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
+                RowFreq fr;
+                row_frequencies(pl, s_lut, lane, fr);
+                int32_t *dst = cdf + (row0 + r) * (VOCAB + 1);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[4 * lane + i] = (int32_t)fr.e[i];
+                if (lane == 63) dst[VOCAB] = (int32_t)TOTAL;
+            }
+        }
+    }
+}
+
+// ---- compress: teacher-forced MLP fused with the frequency step ----------
+
+// Workgroups take whole chunks from a work counter; tiles of 128 consecutive
+// steps of one chunk share a 192-token window in LDS.  Output per token:
+// (exclusive cumulative frequency, frequency) of the token actually coded.
+__global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
+                                                             const int64_t *__restrict__ tok_off,
+                                                             const int32_t *__restrict__ lengths,
+                                                             int64_t n_chunks, uint2 *__restrict__ pairs,
+                                                             unsigned int *__restrict__ counter) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
+    __shared__ uint16_t s_tok[R_TILE + WIN];
+    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ int64_t s_unit;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    for (;;) {
+        __syncthreads();
+        if (threadIdx.x == 0) s_unit = (int64_t)atomicAdd(counter, 1u);
+        __syncthreads();
+        const int64_t c = s_unit;
+        if (c >= n_chunks) break;
+        const int32_t L = lengths[c];
+        const uint8_t *tk = tokens + tok_off[c];
+        uint2 *out = pairs + tok_off[c];
+        for (int32_t t0 = 0; t0 < L; t0 += R_TILE) {
+            // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
+            for (int i = threadIdx.x; i < R_TILE + WIN; i += THREADS) {
+                const int32_t pos = t0 - WIN + i;
+                s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
+            }
+            __syncthreads();
+            mlp_rows<RT_TILE, 2>(M, s_emb, s_act, [&](int r, int p) { return (int)s_tok[r + p]; },
+                              wave, lane);
+            const int32_t valid = min(R_TILE, L - t0);
+            for (int r = wave; r < valid; r += WAVES) {
+                const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
+                RowFreq fr;
+                row_frequencies(pl, s_lut, lane, fr);
+                const int s = s_tok[r + WIN];
+                if ((s >> 2) == lane) {
+                    uint32_t ce = fr.e[0], cf = fr.f[0];
+#pragma unroll
+                    for (int i = 1; i < 4; ++i)
+                        if ((s & 3) == i) { ce = fr.e[i]; cf = fr.f[i]; }
+                    out[t0 + r] = make_uint2(ce, cf);
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// One thread per chunk walks its (cum, freq) pairs through the range coder
+// and seals the stream (cpu_entropy_coding.py:121-227).
+__global__ __launch_bounds__(256) void k_encode_pairs(const uint2 *__restrict__ pairs,
+                                                      const int64_t *__restrict__ tok_off,
+                                                      const int32_t *__restrict__ lengths, int64_t n_chunks,
+                                                      uint32_t *__restrict__ words,
+                                                      const int64_t *__restrict__ word_off,
+                                                      const int32_t *__restrict__ word_cap,
+                                                      int32_t *__restrict__ word_cnt,
+                                                      int32_t *__restrict__ status) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n_chunks) return;
+    const int32_t L = lengths[c];
+    const int32_t cap = word_cap[c];
+    const uint2 *p = pairs + tok_off[c];
+    uint32_t *out = words + word_off[c];
+    EncState s{0ull, ~0ull, 0, 0u, 0};
+    int st = 0;
+    uint2 nxt = L > 0 ? p[0] : make_uint2(0u, 0u);
+    for (int32_t t = 0; t < L; ++t) {
+        const uint2 cur = nxt;
+        if (t + 1 < L) nxt = p[t + 1];
+        if (enc_step(s, cur.x, cur.y, out, cap)) { st = SC_STATUS_CAPACITY; break; }
+    }
+    if (!st && L > 0 && enc_seal(s, out, cap)) st = SC_STATUS_CAPACITY;
+    word_cnt[c] = s.pos;
+    status[c] = st;
+}
+
+__global__ void k_zero_u32(unsigned int *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// ---- decompress: persistent autoregressive loop per chunk tile ----------
+
+// Workgroup b owns chunks [b*R, b*R + R).  Each step: MLP on the R context
+// windows (kept as 64-token rings in LDS), the fused frequency step and one
+// decoder step per chunk; the decoded token is appended to the ring.  Chunks
+// are independent, so workgroups never synchronise with each other.
+template <int RT>
+__global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
+                                                           const int64_t *__restrict__ word_off,
+                                                           const int32_t *__restrict__ word_cnt,
+                                                           const int32_t *__restrict__ lengths,
+                                                           int64_t n_chunks, uint8_t *__restrict__ tokens,
+                                                           const int64_t *__restrict__ tok_off,
+                                                           int32_t *__restrict__ status) {
+    constexpr int R = 32 * RT;
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R * ACT_ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
+    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
+    __shared__ int64_t s_woff[R], s_toff[R];
+    __shared__ int32_t s_rpos[R], s_wcnt[R], s_len[R], s_stat[R];
+    __shared__ int32_t s_maxlen;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t c0 = (int64_t)blockIdx.x * R;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    if (threadIdx.x == 0) s_maxlen = 0;
+    __syncthreads();
+    for (int r = threadIdx.x; r < R; r += THREADS) {
+        const int64_t c = c0 + r;
+        int32_t len = 0, cnt = 0;
+        int64_t woff = 0, toff = 0;
+        if (c < n_chunks) {
+            len = lengths[c];
+            cnt = word_cnt[c];
+            woff = word_off[c];
+            toff = tok_off[c];
+        }
+        // CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474)
+        uint64_t point = 0;
+        const int take = cnt < 2 ? cnt : 2;
+        for (int i = 0; i < take; ++i) point = (point << 32) | words[woff + i];
+        if (cnt == 1) point <<= 32;
+        s_lower[r] = 0ull;
+        s_range[r] = ~0ull;
+        s_point[r] = point;
+        s_rpos[r] = take;
+        s_wcnt[r] = cnt;
+        s_woff[r] = woff;
+        s_toff[r] = toff;
+        s_len[r] = len;
+        s_stat[r] = 0;
+        atomicMax(&s_maxlen, len);
+    }
+    __syncthreads();
+    const int32_t maxlen = s_maxlen;
+    for (int32_t t = 0; t < maxlen; ++t) {
+        mlp_rows<RT, 2>(M, s_emb, s_act,
+                     [&](int r, int p) {
+                         return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
+                     },
+                     wave, lane);
+        for (int r = wave; r < R; r += WAVES) {
+            if (t >= s_len[r] || s_stat[r]) continue;
+            const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
+            RowFreq fr;
+            row_frequencies(pl, s_lut, lane, fr);
+            // _decode_partition (cpu_entropy_coding.py:230-266)
+            uint64_t lower = s_lower[r], range = s_range[r], point = s_point[r];
+            const uint64_t scale = range >> 24;
+            uint32_t q = 0;
+            const bool ok = scale != 0 && dec_quantile(point - lower, scale, q);
+            if (!ok) {
+                if (lane == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
+                continue;
+            }
+            uint32_t cum, freq;
+            const int sym = dec_symbol(fr, q, lane, cum, freq);
+            lower += scale * cum;
+            range = scale * freq;
+            int32_t rpos = s_rpos[r];
+            if (range < (1ull << 32)) {
+                lower <<= 32;
+                range <<= 32;
+                point <<= 32;
+                if (rpos < s_wcnt[r]) point |= words[s_woff[r] + rpos];
+                rpos += 1;
+            }
+            if (lane == 0) {
+                s_lower[r] = lower;
+                s_range[r] = range;
+                s_point[r] = point;
+                s_rpos[r] = rpos;
+                s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
+                tokens[s_toff[r] + t] = (uint8_t)sym;
+            }
+        }
+        __syncthreads();
+    }
+    for (int r = threadIdx.x; r < R; r += THREADS)
+        if (c0 + r < n_chunks) status[c0 + r] = s_stat[r];
+}
+
+// ---- step-API kernels (GpuRangeStepEncoder / GpuRangeDecoder) ------------
+
+__device__ __forceinline__ void stage_lut(const uint64_t *lut, uint64_t *s_lut) {
+    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = lut[i];
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict__ logits, int64_t rows,
+                                                       const uint64_t *__restrict__ lut,
+                                                       int64_t *__restrict__ cdf) {
+    __shared__ uint64_t s_lut[VOCAB];
+    stage_lut(lut, s_lut);
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    RowFreq fr;
+    row_frequencies(*(const uint32_t *)(logits + r * VOCAB + 4 * lane), s_lut, lane, fr);
+    int64_t *dst = cdf + r * (VOCAB + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[4 * lane + i] = fr.e[i];
+    if (lane == 63) dst[VOCAB] = TOTAL;
+}
+
+struct EncArrays {
+    uint64_t *lower, *range;
+    int32_t *inverted;
+    uint32_t *first;
+    int32_t *write_pos, *status;
+};
+
+__global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ logits,
+                                                     const uint64_t *__restrict__ lut,
+                                                     const int64_t *__restrict__ symbols,
+                                                     const int64_t *__restrict__ valid, int64_t t,
+                                                     int64_t B, EncArrays st, uint32_t *__restrict__ words,
+                                                     int64_t max_words) {
+    __shared__ uint64_t s_lut[VOCAB];
+    stage_lut(lut, s_lut);
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= B || t >= valid[b] || st.status[b]) return;
+    const int64_t sym = symbols[b];
+    if (sym < 0 || sym >= VOCAB) {
+        if (lane == 0) st.status[b] = SC_STATUS_BAD_TOKEN;
+        return;
+    }
+    RowFreq fr;
+    row_frequencies(*(const uint32_t *)(logits + b * VOCAB + 4 * lane), s_lut, lane, fr);
+    const int s = (int)sym;
+    const uint32_t cum = (uint32_t)__shfl((int)(s & 3) == 0 ? (int)fr.e[0] : (s & 3) == 1 ? (int)fr.e[1]
+                                                          : (s & 3) == 2 ? (int)fr.e[2] : (int)fr.e[3],
+                                          s >> 2);
+    const uint32_t freq = (uint32_t)__shfl((int)(s & 3) == 0 ? (int)fr.f[0] : (s & 3) == 1 ? (int)fr.f[1]
+                                                           : (s & 3) == 2 ? (int)fr.f[2] : (int)fr.f[3],
+                                           s >> 2);
+    if (lane == 0) {
+        EncState e{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
+        if (enc_step(e, cum, freq, words + b * max_words, (int32_t)max_words)) {
+            st.status[b] = SC_STATUS_CAPACITY;
+            return;
+        }
+        st.lower[b] = e.lower;
+        st.range[b] = e.range;
+        st.inverted[b] = e.inverted;
+        st.first[b] = e.first;
+        st.write_pos[b] = e.pos;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_encode_seal(int64_t B, EncArrays st, uint32_t *__restrict__ words,
+                                                     int64_t max_words) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B || st.status[b]) return;
+    EncState e{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
+    if (enc_seal(e, words + b * max_words, (int32_t)max_words)) {
+        st.status[b] = SC_STATUS_CAPACITY;
+        return;
+    }
+    st.lower[b] = e.lower;
+    st.range[b] = e.range;
+    st.inverted[b] = e.inverted;
+    st.write_pos[b] = e.pos;
+}
+
+struct DecArrays {
+    uint64_t *lower, *range, *point;
+    int64_t *read_pos;
+    const int64_t *end_pos;
+    int32_t *status;
+};
+
+__global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ logits,
+                                                     const uint64_t *__restrict__ lut,
+                                                     const int64_t *__restrict__ valid, int64_t t,
+                                                     int64_t B, DecArrays st,
+                                                     const uint32_t *__restrict__ words,
+                                                     int64_t *__restrict__ symbols_out) {
+    __shared__ uint64_t s_lut[VOCAB];
+    stage_lut(lut, s_lut);
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= B) return;
+    if (t >= valid[b] || st.status[b]) {
+        if (lane == 0) symbols_out[b] = VOCAB;
+        return;
+    }
+    uint64_t lower = st.lower[b], range = st.range[b], point = st.point[b];
+    const uint64_t scale = range >> 24;
+    uint32_t q = 0;
+    if (scale == 0 || !dec_quantile(point - lower, scale, q)) {
+        if (lane == 0) {
+            st.status[b] = SC_STATUS_INVALID_STREAM;
+            symbols_out[b] = VOCAB;
+        }
+        return;
+    }
+    RowFreq fr;
+    row_frequencies(*(const uint32_t *)(logits + b * VOCAB + 4 * lane), s_lut, lane, fr);
+    uint32_t cum, freq;
+    const int sym = dec_symbol(fr, q, lane, cum, freq);
+    lower += scale * cum;
+    range = scale * freq;
+    int64_t rp = st.read_pos[b];
+    if (range < (1ull << 32)) {
+        lower <<= 32;
+        range <<= 32;
+        point <<= 32;
+        if (rp < st.end_pos[b]) point |= words[rp];
+        rp += 1;
+    }
+    if (lane == 0) {
+        st.lower[b] = lower;
+        st.range[b] = range;
+        st.point[b] = point;
+        st.read_pos[b] = rp;
+        symbols_out[b] = sym;
+    }
+}
+
+}  // namespace
+
+// =========================================================================
+// Host side
+// =========================================================================
+
+struct sc_model {
+    int device = 0;
+    int n_cu = 0;
+    ModelDev dev{};
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+thread_local std::string g_err = "";
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(SC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define SC_HIP(call, what)                          \
+    do {                                            \
+        hipError_t e_ = (call);                     \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return SC_OK;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+template <class T>
+int upload(sc_model *m, const std::vector<T> &host, const T **out) {
+    void *p = nullptr;
+    SC_HIP(hipMalloc(&p, host.size() * sizeof(T)), "hipMalloc");
+    m->allocs.push_back(p);
+    SC_HIP(hipMemcpy(p, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy");
+    *out = (const T *)p;
+    return SC_OK;
+}
+
+// Pack W [n, k] into MFMA A-operand fragments: fragment (nt, kt) holds, for
+// lane l, W[nt*32 + l%32][kt*32 + (l/32)*16 .. +16].
+std::vector<int8_t> pack_weight(const int8_t *w, int n, int k) {
+    const int NT = n / 32, KT = k / 32;
+    std::vector<int8_t> out((size_t)n * k + WEIGHT_PAD_FRAGS * 64 * 16, 0);
+    for (int nt = 0; nt < NT; ++nt)
+        for (int kt = 0; kt < KT; ++kt)
+            for (int l = 0; l < 64; ++l)
+                for (int b = 0; b < 16; ++b)
+                    out[(((size_t)nt * KT + kt) * 64 + l) * 16 + b] =
+                        w[(size_t)(nt * 32 + (l & 31)) * k + kt * 32 + (l >> 5) * 16 + b];
+    return out;
+}
+
+hipStream_t as_stream(void *s) { return (hipStream_t)s; }
+
+}  // namespace
+
+extern "C" {
+
+const char *sc_last_error(void) { return g_err.c_str(); }
+
+const char *sc_version(void) { return "sigcomp-hip 0.1 gfx950"; }
+
+int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_t window,
+                    const sc_layer_desc *layers, int32_t n_layers, const int64_t *exp_lut,
+                    int32_t device, sc_model **out) {
+    if (!out || !emb || !layers || !exp_lut) return fail(SC_ERR_ARG, "null argument");
+    *out = nullptr;
+    if (emb_rows != EMB_ROWS || emb_dim != EDIM || window != WIN)
+        return fail(SC_ERR_UNSUPPORTED, "kernels support window 64 and a 257 x 128 embedding");
+    if (n_layers < 2 || n_layers > MAX_LAYERS)
+        return fail(SC_ERR_UNSUPPORTED, "kernels support 2..16 linear layers");
+    for (int i = 0; i < n_layers; ++i) {
+        const sc_layer_desc &L = layers[i];
+        const int want_k = i == 0 ? K0 : HID;
+        const int want_n = i == n_layers - 1 ? VOCAB : HID;
+        if (L.k != want_k || L.n != want_n)
+            return fail(SC_ERR_UNSUPPORTED, "kernels support 8192->512, 512->512 ..., 512->256 layers");
+        if (!L.weight || !L.bias || !L.m0 || !L.shift) return fail(SC_ERR_ARG, "null layer array");
+        for (int j = 0; j < L.n; ++j) {
+            if (L.m0[j] < 0 || L.m0[j] > (int64_t(1) << 31))
+                return fail(SC_ERR_ARG, "requant multiplier outside [0, 2**31]");
+            if (L.shift[j] < 0 || L.shift[j] > 63) return fail(SC_ERR_ARG, "requant shift outside [0, 63]");
+        }
+    }
+    for (int i = 0; i < VOCAB; ++i)
+        if (exp_lut[i] < 0 || exp_lut[i] > (int64_t(1) << 38) || (i == 0 && exp_lut[0] <= 0))
+            return fail(SC_ERR_ARG, "exp_lut must be nonnegative, at most 2**38, and start positive");
+    int n_dev = 0;
+    SC_HIP(hipGetDeviceCount(&n_dev), "hipGetDeviceCount");
+    if (device < 0 || device >= n_dev) return fail(SC_ERR_ARG, "no such device");
+    DeviceGuard guard(device);
+    sc_model *m = new sc_model();
+    m->device = device;
+    hipDeviceProp_t prop;
+    hipError_t pe = hipGetDeviceProperties(&prop, device);
+    if (pe != hipSuccess) {
+        delete m;
+        return hip_fail(pe, "hipGetDeviceProperties");
+    }
+    m->n_cu = prop.multiProcessorCount;
+    int rc = SC_OK;
+    {
+        std::vector<int8_t> e(emb, emb + EMB_ROWS * EDIM);
+        rc = upload(m, e, &m->dev.emb);
+    }
+    if (rc == SC_OK) {
+        std::vector<uint64_t> lut(exp_lut, exp_lut + VOCAB);
+        rc = upload(m, lut, &m->dev.lut);
+    }
+    for (int i = 0; i < n_layers && rc == SC_OK; ++i) {
+        const sc_layer_desc &L = layers[i];
+        LayerDev &D = m->dev.layer[i];
+        std::vector<int8_t> packed = pack_weight(L.weight, L.n, L.k);
+        const int8_t *wdev = nullptr;
+        rc = upload(m, packed, &wdev);
+        D.w = (const v4i *)wdev;
+        if (rc) break;
+        std::vector<int32_t> bias(L.bias, L.bias + L.n);
+        rc = upload(m, bias, &D.bias);
+        if (rc) break;
+        std::vector<uint32_t> m0(L.n);
+        std::vector<uint8_t> sh(L.n);
+        for (int j = 0; j < L.n; ++j) {
+            m0[j] = (uint32_t)L.m0[j];
+            sh[j] = (uint8_t)L.shift[j];
+        }
+        rc = upload(m, m0, &D.m0);
+        if (rc) break;
+        rc = upload(m, sh, &D.shift);
+        D.n = L.n;
+        D.kt = L.k / 32;
+        D.relu = L.relu ? 1 : 0;
+        D.bytes = (int32_t)packed.size();
+    }
+    m->dev.n_layers = n_layers;
+    if (rc != SC_OK) {
+        sc_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return SC_OK;
+}
+
+int sc_model_destroy(sc_model *m) {
+    if (!m) return SC_OK;
+    DeviceGuard guard(m->device);
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+    return SC_OK;
+}
+
+const uint64_t *sc_model_lut(const sc_model *m) { return m ? m->dev.lut : nullptr; }
+
+static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t rows, int8_t *logits,
+                              int32_t *cdf, int32_t *status, void *stream, int mode) {
+    if (!m || rows < 0 || !status) return fail(SC_ERR_ARG, "bad argument");
+    if (rows == 0) return SC_OK;
+    if (!ctx || (mode == OUT_LOGITS && !logits) || (mode == OUT_CDF32 && !cdf))
+        return fail(SC_ERR_ARG, "null device pointer");
+    DeviceGuard guard(m->device);
+    const int64_t tiles = (rows + R_TILE - 1) / R_TILE;
+    const int grid = (int)std::min<int64_t>(tiles, m->n_cu);
+    if (mode == OUT_LOGITS)
+        hipLaunchKernelGGL(k_mlp_context<OUT_LOGITS>, dim3(grid), dim3(THREADS), 0, as_stream(stream),
+                           m->dev, ctx, rows, logits, cdf, status);
+    else
+        hipLaunchKernelGGL(k_mlp_context<OUT_CDF32>, dim3(grid), dim3(THREADS), 0, as_stream(stream),
+                           m->dev, ctx, rows, logits, cdf, status);
+    return check_launch("k_mlp_context");
+}
+
+int sc_mlp_forward(const sc_model *m, const int64_t *ctx, int64_t rows, int8_t *logits, int32_t *status,
+                   void *stream) {
+    return mlp_context_launch(m, ctx, rows, logits, nullptr, status, stream, OUT_LOGITS);
+}
+
+int sc_mlp_forward_cdf(const sc_model *m, const int64_t *ctx, int64_t rows, int32_t *cdf, int32_t *status,
+                       void *stream) {
+    return mlp_context_launch(m, ctx, rows, nullptr, cdf, status, stream, OUT_CDF32);
+}
+
+int sc_logits_to_cdf(const int8_t *logits, int64_t rows, const uint64_t *lut, int64_t *cdf, void *stream) {
+    if (rows < 0) return fail(SC_ERR_ARG, "rows must be nonnegative");
+    if (rows == 0) return SC_OK;
+    if (!logits || !lut || !cdf) return fail(SC_ERR_ARG, "null device pointer");
+    hipLaunchKernelGGL(k_logits_to_cdf, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, as_stream(stream),
+                       logits, rows, lut, cdf);
+    return check_launch("k_logits_to_cdf");
+}
+
+static bool enc_ok(const sc_encoder_state *s) {
+    return s && s->lower && s->range && s->inverted && s->first && s->write_pos && s->status;
+}
+
+int sc_encode_step(const int8_t *logits, const uint64_t *lut, const int64_t *symbols, const int64_t *valid_lens,
+                   int64_t t, int64_t B, const sc_encoder_state *state, uint32_t *words, int64_t max_words,
+                   void *stream) {
+    if (B < 0 || t < 0 || max_words < 2 || max_words > INT32_MAX) return fail(SC_ERR_ARG, "bad sizes");
+    if (B == 0) return SC_OK;
+    if (!logits || !lut || !symbols || !valid_lens || !words || !enc_ok(state))
+        return fail(SC_ERR_ARG, "null device pointer");
+    EncArrays a{state->lower, state->range, state->inverted, state->first, state->write_pos, state->status};
+    hipLaunchKernelGGL(k_encode_step, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, as_stream(stream), logits, lut,
+                       symbols, valid_lens, t, B, a, words, max_words);
+    return check_launch("k_encode_step");
+}
+
+int sc_encode_seal(int64_t B, const sc_encoder_state *state, uint32_t *words, int64_t max_words, void *stream) {
+    if (B < 0 || max_words < 2 || max_words > INT32_MAX) return fail(SC_ERR_ARG, "bad sizes");
+    if (B == 0) return SC_OK;
+    if (!words || !enc_ok(state)) return fail(SC_ERR_ARG, "null device pointer");
+    EncArrays a{state->lower, state->range, state->inverted, state->first, state->write_pos, state->status};
+    hipLaunchKernelGGL(k_encode_seal, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, as_stream(stream), B, a,
+                       words, max_words);
+    return check_launch("k_encode_seal");
+}
+
+int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *valid_lens, int64_t t, int64_t B,
+                   const sc_decoder_state *state, const uint32_t *words, int64_t *symbols_out, void *stream) {
+    if (B < 0 || t < 0) return fail(SC_ERR_ARG, "bad sizes");
+    if (B == 0) return SC_OK;
+    if (!logits || !lut || !valid_lens || !symbols_out || !state || !state->lower || !state->range ||
+        !state->point || !state->read_pos || !state->end_pos || !state->status || !words)
+        return fail(SC_ERR_ARG, "null device pointer");
+    DecArrays a{state->lower, state->range, state->point, state->read_pos, state->end_pos, state->status};
+    hipLaunchKernelGGL(k_decode_step, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, as_stream(stream), logits, lut,
+                       valid_lens, t, B, a, words, symbols_out);
+    return check_launch("k_decode_step");
+}
+
+int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks) {
+    (void)n_chunks;
+    if (n_tokens < 0) return -1;
+    return 256 + ((n_tokens * 8 + 255) / 256) * 256;
+}
+
+int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *tok_off, const int32_t *lengths,
+                       int64_t n_chunks, int64_t n_tokens, uint32_t *words, const int64_t *word_off,
+                       const int32_t *word_cap, int32_t *word_cnt, int32_t *status, void *workspace,
+                       int64_t workspace_bytes, void *stream) {
+    if (!m || n_chunks < 0 || n_tokens < 0) return fail(SC_ERR_ARG, "bad argument");
+    if (n_chunks == 0) return SC_OK;
+    if (!tokens || !tok_off || !lengths || !words || !word_off || !word_cap || !word_cnt || !status || !workspace)
+        return fail(SC_ERR_ARG, "null device pointer");
+    if (workspace_bytes < sc_compress_workspace_bytes(n_tokens, n_chunks))
+        return fail(SC_ERR_ARG, "workspace too small");
+    DeviceGuard guard(m->device);
+    unsigned int *counter = (unsigned int *)workspace;
+    uint2 *pairs = (uint2 *)((char *)workspace + 256);
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, s, counter, 64);
+    int rc = check_launch("k_zero_u32");
+    if (rc) return rc;
+    const int grid = (int)std::min<int64_t>(n_chunks, m->n_cu);
+    hipLaunchKernelGGL(k_compress_mlp, dim3(grid), dim3(THREADS), 0, s, m->dev, tokens, tok_off, lengths, n_chunks,
+                       pairs, counter);
+    rc = check_launch("k_compress_mlp");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_encode_pairs, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, pairs, tok_off,
+                       lengths, n_chunks, words, word_off, word_cap, word_cnt, status);
+    return check_launch("k_encode_pairs");
+}
+
+int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt,
+                         const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
+                         int32_t *status, void *stream) {
+    if (!m || n_chunks < 0) return fail(SC_ERR_ARG, "bad argument");
+    if (n_chunks == 0) return SC_OK;
+    if (!words || !word_off || !word_cnt || !lengths || !tokens || !tok_off || !status)
+        return fail(SC_ERR_ARG, "null device pointer");
+    DeviceGuard guard(m->device);
+    // rows per workgroup: enough 32-row tiles that one wave of workgroups
+    // covers every chunk, at most DEC_RT_MAX tiles
+    int64_t rt = (n_chunks + 32LL * m->n_cu - 1) / (32LL * m->n_cu);
+    rt = std::max<int64_t>(1, std::min<int64_t>(rt, DEC_RT_MAX));
+    const int64_t R = 32 * rt;
+    const unsigned grid = (unsigned)((n_chunks + R - 1) / R);
+    hipStream_t s = as_stream(stream);
+    switch (rt) {
+#define SC_DEC_CASE(N)                                                                                         \
+    case N:                                                                                                    \
+        hipLaunchKernelGGL(k_decompress<N>, dim3(grid), dim3(THREADS), 0, s, m->dev, words, word_off, word_cnt, \
+                           lengths, n_chunks, tokens, tok_off, status);                                        \
+        break;
+        SC_DEC_CASE(1)
+        SC_DEC_CASE(2)
+        SC_DEC_CASE(3)
+        SC_DEC_CASE(4)
+#undef SC_DEC_CASE
+    }
+    return check_launch("k_decompress");
+}
+
+}  // extern "C"

@@ -1,0 +1,257 @@
+"""GPU codec: drop-in for the reference's ``QuantMLPCompression``.
+
+Mirrors ``quant_mlp_export.py`` of the reference (``QuantMLPCompression``
+:210-377, ``GPUBitExactMLPDecoder`` :113-141): constructed with
+``(chunk_len, gpu, model_path, dim, num_dec_layers, window_size)``, exposing
+``compress_chunks`` / ``decompress_chunks`` and, through
+``ReadFramingMixin``, ``batch_inference_reads``.  The work runs in the gfx950
+kernels of ``libsigcomp_hip.so``:
+
+* compress: one persistent kernel runs the teacher-forced MLP over every
+  step of every chunk (all tokens are known) fused with the logits ->
+  frequency step, then one thread per chunk runs the range encoder and seal;
+* decompress: one persistent kernel in which each workgroup owns a tile of
+  chunks and runs the whole autoregressive loop for them on chip.
+
+Chunk bytes equal ``CPUQuantMLPCompression``'s (``cpu_compression.py:178-332``).
+``max_batch_size`` bounds host staging only: chunks are independent, so the
+batch split does not change any output byte.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _hip
+from .framing import ReadFramingMixin, as_symbols
+from .model_io import (DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH,  # noqa: F401
+                       DEFAULT_QUANT_MODEL_PATH, DEFAULT_LSB_SETTING_FOR_LOSSY_MODEL, IntModel,
+                       SOS_TOKEN, VOCAB_SIZE, load_int_model)
+
+# Chunks staged per kernel launch (bounds host/device staging memory only).
+_MIN_LAUNCH_CHUNKS = 1 << 16
+
+
+class HipModel:
+    """An ``IntModel`` uploaded to one GPU (owns the ``sc_model`` handle)."""
+
+    def __init__(self, model: IntModel, device: torch.device):
+        self.model = model
+        self.device = torch.device(device)
+        self.window = int(model.window)
+        layers = (_hip.LayerDesc * len(model.layers))()
+        keep = []
+        for i, L in enumerate(model.layers):
+            arrs = [np.ascontiguousarray(L.weight, np.int8), np.ascontiguousarray(L.bias, np.int32),
+                    np.ascontiguousarray(L.m0, np.int64), np.ascontiguousarray(L.shift, np.int32)]
+            keep.extend(arrs)
+            layers[i] = _hip.LayerDesc(L.n, L.k, arrs[0].ctypes.data, arrs[1].ctypes.data,
+                                       arrs[2].ctypes.data, arrs[3].ctypes.data, int(L.relu))
+        emb = np.ascontiguousarray(model.emb, np.int8)
+        lut = np.ascontiguousarray(model.exp_lut, np.int64)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _hip.check(_hip.lib().sc_model_create(emb.ctypes.data, emb.shape[0], emb.shape[1],
+                                                  self.window, layers, len(model.layers),
+                                                  lut.ctypes.data, self.device.index or 0,
+                                                  ctypes.byref(handle)))
+        self.handle = handle
+        self.exp_lut = torch.from_numpy(lut.copy()).to(self.device)
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                _hip.lib().sc_model_destroy(h)
+            except Exception:
+                pass
+            self.handle = None
+
+    # ---- explicit windows -------------------------------------------------
+
+    def forward_windows(self, ctx: torch.Tensor, out: str = "logits") -> torch.Tensor:
+        """ctx int64 [rows, window] (device) -> int8 logits [rows, 256] or int32 CDF [rows, 257]."""
+        if ctx.ndim != 2 or ctx.shape[1] != self.window:
+            raise ValueError("context_window must be shaped [batch, window_size]")
+        ctx = ctx.to(self.device, torch.int64).contiguous()
+        rows = ctx.shape[0]
+        status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        with torch.cuda.device(self.device):
+            if out == "logits":
+                res = torch.empty((rows, VOCAB_SIZE), dtype=torch.int8, device=self.device)
+                fn = _hip.lib().sc_mlp_forward
+            else:
+                res = torch.empty((rows, VOCAB_SIZE + 1), dtype=torch.int32, device=self.device)
+                fn = _hip.lib().sc_mlp_forward_cdf
+            _hip.check(fn(self.handle, _hip.ptr(ctx), rows, _hip.ptr(res), _hip.ptr(status),
+                          _hip.stream_ptr()))
+        if int(status.item()) != 0:
+            raise ValueError("context tokens must be in [0, 256]")
+        return res
+
+
+class GPUBitExactMLPDecoder:
+    """``quant_mlp_export.py:113-141``: the integer MLP on explicit windows."""
+
+    def __init__(self, hip_model: HipModel, output_scale: float):
+        self.hip = hip_model
+        self.window_size = hip_model.window
+        self.vocab_size = SOS_TOKEN + 1
+        self.output_scale = torch.tensor(float(output_scale), dtype=torch.float32)
+
+    def eval(self):
+        return self
+
+    def _ar_step(self, context_window: torch.Tensor) -> torch.Tensor:
+        """context int64 [B, 64] -> int8 logits [B, 1, 256]."""
+        return self.hip.forward_windows(context_window, "logits").unsqueeze(1)
+
+    def forward(self, targets: torch.Tensor) -> torch.Tensor:
+        """Teacher-forced logits [B, L, 256]; windows pad with the first target
+        token repeated, as ``quant_mlp_export.py:122-130`` does."""
+        B, L = targets.shape
+        targets = targets.to(self.hip.device, torch.int64)
+        pad = targets[:, :1].expand(-1, self.window_size - 1)
+        windows = torch.cat([pad, targets], dim=1).unfold(1, self.window_size, 1)
+        out = self.hip.forward_windows(windows.reshape(-1, self.window_size), "logits")
+        return out.view(B, L, VOCAB_SIZE)
+
+    def dequantize_logits(self, int8_logits):
+        return int8_logits.float() * self.output_scale.to(int8_logits.device)
+
+
+class QuantMLPCompression(ReadFramingMixin):
+    DEFAULT_DIM = 256
+    DEFAULT_NUM_DEC_LAYERS = 8
+    DEFAULT_WINDOW_SIZE = 64
+
+    def __init__(self, chunk_len=1024, gpu=0, model_path=None, dim=None, num_dec_layers=None,
+                 window_size=None, *, model: IntModel | None = None):
+        if chunk_len < 1:
+            raise ValueError("chunk_len must be positive")
+        dim = dim or self.DEFAULT_DIM
+        num_dec_layers = num_dec_layers or self.DEFAULT_NUM_DEC_LAYERS
+        window_size = window_size or self.DEFAULT_WINDOW_SIZE
+        if model is None:
+            model = load_int_model(model_path or DEFAULT_QUANT_MODEL_PATH, dim, num_dec_layers,
+                                   window_size)
+        self.gpu = int(gpu)
+        self.device = f"cuda:{self.gpu}"
+        self.SOS_token = SOS_TOKEN
+        self.window_size = int(model.window)
+        self.chunk_len = int(chunk_len)
+        self.model = model
+        self.hip = HipModel(model, torch.device(self.device))
+        self.gpu_engine = GPUBitExactMLPDecoder(self.hip, model.output_scale)
+        self._exp_lut = self.hip.exp_lut
+        self.last_timing = {}
+
+    # ------------------------------------------------------------ compress
+
+    def compress_chunks(self, chunks, max_batch_size=64, use_perfect=False, use_tqdm=False):
+        if max_batch_size < 1:
+            raise ValueError("max_batch_size must be positive")
+        chunks = [as_symbols(c) for c in chunks]
+        if any(len(c) > self.chunk_len for c in chunks):
+            raise ValueError("A token chunk exceeds chunk_len")
+        per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
+        out = []
+        for s in range(0, len(chunks), per):
+            out.extend(self._compress_batch(chunks[s:s + per]))
+        return out
+
+    def _compress_batch(self, chunks):
+        n = len(chunks)
+        if n == 0:
+            return []
+        lengths = np.fromiter((len(c) for c in chunks), dtype=np.int32, count=n)
+        tok_off = np.zeros(n, dtype=np.int64)
+        np.cumsum(lengths[:-1], out=tok_off[1:])
+        n_tokens = int(lengths.sum())
+        tokens = np.concatenate(chunks) if n_tokens else np.zeros(1, np.uint8)
+        cap = lengths + 2
+        word_off = np.zeros(n, dtype=np.int64)
+        np.cumsum(cap[:-1], dtype=np.int64, out=word_off[1:])
+        dev = self.hip.device
+        d = lambda a: torch.from_numpy(a).to(dev, non_blocking=False)
+        t_tokens, t_tok_off, t_len = d(tokens), d(tok_off), d(lengths)
+        t_word_off, t_cap = d(word_off), d(cap.astype(np.int32))
+        words, cnt, status, ws = self._compress_buffers(n, n_tokens, int(cap.sum()))
+        with torch.cuda.device(dev):
+            _hip.check(_hip.lib().sc_compress_chunks(
+                self.hip.handle, _hip.ptr(t_tokens), _hip.ptr(t_tok_off), _hip.ptr(t_len), n,
+                n_tokens, _hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(t_cap), _hip.ptr(cnt),
+                _hip.ptr(status), _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
+        st = status.cpu().numpy()
+        if st.any():
+            b = int(np.flatnonzero(st)[0])
+            raise OverflowError(f"range-coder output capacity exceeded in stream {b}")
+        cnt_np = cnt.cpu().numpy()
+        words_np = words.cpu().numpy()
+        return [words_np[word_off[i]:word_off[i] + cnt_np[i]].tobytes() for i in range(n)]
+
+    def _compress_buffers(self, n, n_tokens, n_words):
+        dev = self.hip.device
+        ws_bytes = int(_hip.lib().sc_compress_workspace_bytes(n_tokens, n))
+        words = torch.empty(max(n_words, 1), dtype=torch.int32, device=dev)
+        cnt = torch.empty(n, dtype=torch.int32, device=dev)
+        status = torch.empty(n, dtype=torch.int32, device=dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        return words, cnt, status, ws
+
+    # ---------------------------------------------------------- decompress
+
+    def decompress_chunks(self, compressed_bytes_list, valid_lengths, max_batch_size=64,
+                          use_perfect=False, use_tqdm=False):
+        if max_batch_size < 1:
+            raise ValueError("max_batch_size must be positive")
+        if len(compressed_bytes_list) != len(valid_lengths):
+            raise ValueError("Compressed chunk and length counts differ")
+        if any(int(n) != n or n < 0 or n > self.chunk_len for n in valid_lengths):
+            raise ValueError("Chunk lengths must be integers in [0, chunk_len]")
+        for data, length in zip(compressed_bytes_list, valid_lengths):
+            if (length and (not data or len(data) % 4)) or (not length and data):
+                raise ValueError("Invalid range-coded chunk for its token length")
+        per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
+        out = []
+        for s in range(0, len(compressed_bytes_list), per):
+            out.extend(self._decompress_batch(compressed_bytes_list[s:s + per],
+                                              valid_lengths[s:s + per]))
+        return out
+
+    def _decompress_batch(self, chunk_bytes, valid_lengths):
+        n = len(chunk_bytes)
+        if n == 0:
+            return []
+        lengths = np.asarray(valid_lengths, dtype=np.int32)
+        cnt = np.fromiter((len(b) // 4 for b in chunk_bytes), dtype=np.int32, count=n)
+        word_off = np.zeros(n, dtype=np.int64)
+        np.cumsum(cnt[:-1], dtype=np.int64, out=word_off[1:])
+        flat = (np.frombuffer(b"".join(chunk_bytes), dtype="<u4").astype(np.uint32, copy=False)
+                if cnt.sum() else np.zeros(1, np.uint32))
+        tok_off = np.zeros(n, dtype=np.int64)
+        np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
+        n_tokens = int(lengths.sum())
+        # longest chunks first: every workgroup then holds chunks of similar
+        # length and stops at its own longest one
+        order = np.argsort(-lengths, kind="stable")
+        dev = self.hip.device
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        t_words = d(flat.view(np.int32))
+        t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(lengths[order]), d(tok_off[order])
+        tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)
+        status = torch.empty(n, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            _hip.check(_hip.lib().sc_decompress_chunks(
+                self.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt),
+                _hip.ptr(t_len), n, _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status),
+                _hip.stream_ptr()))
+        st = status.cpu().numpy()
+        if st.any():
+            raise ValueError("invalid range stream or mismatching entropy model in chunk "
+                             f"{int(order[np.flatnonzero(st)[0]])}")
+        tok = tokens.cpu().numpy()
+        return [tok[tok_off[i]:tok_off[i] + lengths[i]].copy() for i in range(n)]

@@ -1,0 +1,182 @@
+"""GPU parity: the gfx950 kernels against the reference golden vectors and the
+CPU oracle, bit-exact (integer / byte work has no tolerance)."""
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def codecs(int_models):
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    return {name: QuantMLPCompression(chunk_len=2048, gpu=0, model=m) for name, m in int_models.items()}
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_ar_step_matches_reference_logits(codecs, name):
+    z = np.load(GOLDEN / f"mlp_{name}.npz")
+    ctx = torch.from_numpy(z["ctx"]).cuda()
+    got = codecs[name].gpu_engine._ar_step(ctx)[:, 0].cpu().numpy()
+    assert np.array_equal(got, z["logits"])
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_fused_mlp_cdf_matches_reference(codecs, name):
+    z = np.load(GOLDEN / f"mlp_{name}.npz")
+    c = np.load(GOLDEN / f"cdf_{name}.npz")
+    n = z["ctx"].shape[0]
+    got = codecs[name].hip.forward_windows(torch.from_numpy(z["ctx"]).cuda(), "cdf").cpu().numpy()
+    assert np.array_equal(got.astype(np.int64), c["cdf"][:n])
+
+
+@pytest.mark.parametrize("rows", [1, 127, 128, 129, 1000])
+def test_ar_step_matches_oracle_random_windows(codecs, oracle_mod, oracle_models, rows):
+    rng = np.random.default_rng(rows)
+    ctx = rng.integers(0, 257, (rows, 64))
+    ctx[: rows // 3, : 20] = 256
+    got = codecs["lossless"].gpu_engine._ar_step(torch.from_numpy(ctx).cuda())[:, 0].cpu().numpy()
+    assert np.array_equal(got, oracle_mod.mlp_forward(oracle_models["lossless"], ctx))
+
+
+def test_random_per_channel_model_matches_oracle(oracle_mod):
+    from sigcomp_amd.model_io import random_int_model
+    from sigcomp_amd.quant_mlp_export import HipModel
+    m = random_int_model(seed=7, per_channel=True)
+    hm = HipModel(m, torch.device("cuda:0"))
+    rng = np.random.default_rng(9)
+    ctx = rng.integers(0, 257, (300, 64))
+    got = hm.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
+    om = oracle_mod.OracleModel(m)
+    exp = oracle_mod.mlp_forward(om, ctx)
+    assert np.array_equal(got, exp)
+    assert len(np.unique(exp)) > 50          # activations are not saturated
+    cdf = hm.forward_windows(torch.from_numpy(ctx).cuda(), "cdf").cpu().numpy()
+    assert np.array_equal(cdf.astype(np.int64), oracle_mod.logits_to_cdf(exp, m.exp_lut))
+
+
+def test_bad_context_token_raises(codecs):
+    ctx = torch.full((3, 64), 256, dtype=torch.int64, device="cuda")
+    ctx[1, 7] = 300
+    with pytest.raises(ValueError):
+        codecs["lossless"].gpu_engine._ar_step(ctx)
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_int8_logits_to_cdf_matches_reference(int_models, name):
+    from sigcomp_amd.gpu_entropy_coding import int8_logits_to_cdf
+    c = np.load(GOLDEN / f"cdf_{name}.npz")
+    got = int8_logits_to_cdf(torch.from_numpy(c["logits"]).cuda(), int_models[name].exp_lut)
+    assert np.array_equal(got.cpu().numpy(), c["cdf"])
+
+
+def _golden_streams(name):
+    z = np.load(GOLDEN / "coder_streams.npz")
+    keys = sorted({k.rsplit("_", 1)[0] for k in z.files if k.startswith(name + "_")})
+    return z, keys
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_step_encoder_and_decoder_match_reference(int_models, name):
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
+    z, keys = _golden_streams(name)
+    lut = torch.from_numpy(int_models[name].exp_lut)
+    B = len(keys)
+    T = max(len(z[f"{k}_symbols"]) for k in keys)
+    lg = np.zeros((B, T, 256), np.int8)
+    sy = np.zeros((B, T), np.int64)
+    valid = np.array([len(z[f"{k}_symbols"]) for k in keys], np.int64)
+    for b, k in enumerate(keys):
+        lg[b, :valid[b]] = z[f"{k}_logits"]
+        sy[b, :valid[b]] = z[f"{k}_symbols"]
+    enc = GpuRangeStepEncoder(B, T + 32, device="cuda")
+    lg_d = torch.from_numpy(lg).cuda()
+    sy_d = torch.from_numpy(sy).cuda()
+    v_d = torch.from_numpy(valid).cuda()
+    for t in range(T):
+        enc.encode_step_int8(lg_d[:, t], lut, sy_d[:, t], v_d, t)
+    words = enc.get_compressed()
+    for b, k in enumerate(keys):
+        assert np.array_equal(np.frombuffer(words[b], "<u4"), z[f"{k}_words"]), k
+    dec = GpuRangeDecoder(words, device="cuda")
+    got = np.zeros((B, T), np.int64)
+    for t in range(T):
+        got[:, t] = dec.decode_step_int8(lg_d[:, t], lut, v_d, t).cpu().numpy()
+    dec.check()
+    for b, k in enumerate(keys):
+        assert np.array_equal(got[b, :valid[b]], z[f"{k}_decoded"]), k
+        assert np.all(got[b, valid[b]:] == 256)
+
+
+def test_step_decoder_flags_invalid_stream(int_models):
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
+    bad = np.array([0xFFFFFFFF, 0xFFFFFFFF], np.uint32).tobytes()
+    dec = GpuRangeDecoder([bad], device="cuda")
+    lg = torch.zeros((1, 256), dtype=torch.int8, device="cuda")
+    sym = dec.decode_step_int8(lg, int_models["lossless"].exp_lut, torch.tensor([4]), 0)
+    assert int(sym[0]) == 256
+    with pytest.raises(ValueError):
+        dec.check()
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_batch_inference_reads_matches_reference_e2e(codecs, name):
+    from sigcomp_amd import signal
+    z = np.load(GOLDEN / "e2e_reads.npz")
+    lsb = int(z[f"{name}_lsb"])
+    n = int(z[f"{name}_nreads"])
+    small = [signal.split_signal(signal.prepare_signal(z[f"{name}_read{i}_signal"], lsb))[1]
+             for i in range(n)]
+    framed = codecs[name].batch_inference_reads(list_of_reads=small, batch_size=20480)
+    for i in range(n):
+        assert framed[i] == z[f"{name}_read{i}_sbytes"].tobytes(), i
+    back = codecs[name].batch_inference_reads(list_of_compressed_reads=framed,
+                                              list_of_lengths=[len(s) for s in small],
+                                              batch_size=20480)
+    for s, b in zip(small, back):
+        assert np.array_equal(s, b)
+
+
+@pytest.mark.parametrize("lengths", [[1], [2, 63, 64, 65], [127, 128, 129, 300, 2048, 1, 7],
+                                     [2048] * 5 + [5, 1999]])
+def test_compress_decompress_chunks_match_oracle(codecs, oracle_mod, oracle_models, lengths):
+    rng = np.random.default_rng(sum(lengths))
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    chunks[0][: min(3, lengths[0])] = 255
+    gpu = codecs["lossless"].compress_chunks(chunks, max_batch_size=4)
+    ref = oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    assert gpu == ref
+    back = codecs["lossless"].decompress_chunks(gpu, lengths)
+    for c, b in zip(chunks, back):
+        assert np.array_equal(c, b)
+
+
+def test_decompress_many_chunks_round_trip(codecs):
+    """More chunks than one workgroup row tile per CU; mixed lengths."""
+    rng = np.random.default_rng(11)
+    n = 3000
+    lengths = rng.integers(1, 200, n)
+    chunks = [rng.integers(0, 40, L).astype(np.uint8) for L in lengths]
+    comp = codecs["lossy"].compress_chunks(chunks)
+    back = codecs["lossy"].decompress_chunks(comp, list(lengths))
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+
+
+def test_decompress_corrupt_chunk_raises(codecs):
+    bad = [np.array([0xFFFFFFFF, 0xFFFFFFFF], np.uint32).tobytes()]
+    with pytest.raises(ValueError):
+        codecs["lossless"].decompress_chunks(bad, [10])
+
+
+def test_empty_inputs(codecs):
+    assert codecs["lossless"].compress_chunks([]) == []
+    assert codecs["lossless"].decompress_chunks([], []) == []
+    assert codecs["lossless"].batch_inference_reads(list_of_reads=[np.zeros(0, np.uint8)]) == [b""]
+    out = codecs["lossless"].batch_inference_reads(list_of_compressed_reads=[b""], list_of_lengths=[0])
+    assert len(out) == 1 and out[0].size == 0
