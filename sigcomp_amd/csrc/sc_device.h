@@ -32,7 +32,6 @@ constexpr int MAX_LAYERS = 16;
 constexpr uint32_t TOTAL = 1u << 24;    // frequency precision 2**24
 constexpr int ACT_ROW = 512;            // bytes per activation row in LDS
 constexpr int EMB_BYTES = EMB_ROWS * EDIM;
-constexpr int WEIGHT_PAD_FRAGS = 4;      // >= prefetch depth
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -45,6 +44,8 @@ struct LayerDev {
     int32_t n, kt;           // output width, k-tiles of 32
     int32_t relu;
     int32_t bytes;           // size of the packed weight buffer
+    int32_t fast;            // every m0 < 2**31 and shift >= 32; shift[] holds shift - 32
+    int32_t pad;
 };
 
 struct ModelDev {
@@ -125,6 +126,19 @@ __device__ __forceinline__ uint32_t requant_u8(int acc, int bias, uint32_t m0, u
     return (uint32_t)(uint8_t)(int8_t)s;
 }
 
+// The same function when m0 < 2**31 and shift >= 32 (layers flagged `fast`,
+// whose shift array then holds shift - 32): writing the 64-bit product as
+// hi*2**32 + lo with 0 <= lo < 2**32, floor(prod / 2**shift) equals
+// floor(hi / 2**(shift-32)) because the low part adds less than one unit.
+__device__ __forceinline__ uint32_t requant_u8_fast(int acc, int bias, int m0, uint32_t shift32,
+                                                    int lo) {
+    const int biased = (int)((uint32_t)acc + (uint32_t)bias);
+    int s = __mulhi(biased, m0) >> shift32;
+    s = s < lo ? lo : s;
+    s = s > 127 ? 127 : s;
+    return (uint32_t)(uint8_t)(int8_t)s;
+}
+
 // ---------------------------------------------------------------- MFMA GEMMs
 
 template <int NTP, int RT>
@@ -157,11 +171,13 @@ __device__ __forceinline__ v4i wload(const WStream &ws, int voff, int kt) {
 
 // Hidden / output layer: B operand from the activation rows in LDS.
 // The wave computes output n-tiles [nt0, nt0 + NTP) for all RT row tiles.
+// B fragments are read one k-tile ahead of their MFMAs (the read for the
+// step past the end wraps to k-tile 0 and is unused).
 template <int NTP, int RT, int KT>
 __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const uint8_t *s_act,
                                             v16i (&acc)[NTP][RT], int lane) {
     constexpr int PD = 4;
-    static_assert(KT % PD == 0, "k-tiles must be a multiple of the prefetch depth");
+    static_assert(KT % PD == 0 && (KT & (KT - 1)) == 0, "k-tiles: power of two, multiple of PD");
     int voff[NTP];
 #pragma unroll
     for (int j = 0; j < NTP; ++j) voff[j] = (nt0 + j) * KT * 1024 + lane * 16;
@@ -171,6 +187,13 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
 #pragma unroll
         for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], s);
     const int rl = lane & 31, g = lane >> 5;
+    int roff[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) roff[i] = (i * 32 + rl) * ACT_ROW;
+    const int key = rl & 15;   // act_off swizzle key; (i*32 + rl) & 15 == rl & 15
+    v4i bcur[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) bcur[i] = *(const v4i *)(s_act + roff[i] + ((g ^ key) << 4));
 #pragma unroll 1
     for (int kt0 = 0; kt0 < KT; kt0 += PD) {
 #pragma unroll
@@ -179,23 +202,26 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
             v4i a[NTP];
 #pragma unroll
             for (int j = 0; j < NTP; ++j) a[j] = ring[s][j];
-            v4i b[RT];
-            const int c = kt * 2 + g;
+            v4i bnxt[RT];
+            const int cn = (((kt + 1) & (KT - 1)) * 2 + g) ^ key;
 #pragma unroll
-            for (int i = 0; i < RT; ++i) b[i] = *(const v4i *)(s_act + act_off(i * 32 + rl, c));
+            for (int i = 0; i < RT; ++i) bnxt[i] = *(const v4i *)(s_act + roff[i] + (cn << 4));
 #pragma unroll
             for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], kt + PD);
 #pragma unroll
             for (int j = 0; j < NTP; ++j)
 #pragma unroll
                 for (int i = 0; i < RT; ++i)
-                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b[i], acc[j][i], 0, 0, 0);
+                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bcur[i], acc[j][i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) bcur[i] = bnxt[i];
         }
     }
 }
 
 // Layer 0: the B operand row r, k = p*128 + j is emb[tok(r, p)][j], gathered
 // from the LDS embedding table; a k-tile of 32 never straddles a position.
+// Tokens are looked up one position ahead and B fragments one k-tile ahead.
 template <int NTP, int RT, class TokFn>
 __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
                                             TokFn tok, v16i (&acc)[NTP][RT], int lane) {
@@ -209,14 +235,25 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
 #pragma unroll
         for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], s);
     const int rl = lane & 31, g = lane >> 5;
+    int ebase[RT], ekey[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        const int t = tok(i * 32 + rl, 0);
+        ebase[i] = t * EDIM;
+        ekey[i] = t & 7;
+    }
+    v4i bcur[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) bcur[i] = *(const v4i *)(s_emb + ebase[i] + ((g ^ ekey[i]) << 4));
 #pragma unroll 1
     for (int p = 0; p < WIN; ++p) {
-        int ebase[RT], ekey[RT];
+        int nbase[RT], nkey[RT];
+        const int pn = p + 1 < WIN ? p + 1 : WIN - 1;
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
-            const int t = tok(i * 32 + rl, p);
-            ebase[i] = t * EDIM;
-            ekey[i] = t & 7;
+            const int t = tok(i * 32 + rl, pn);
+            nbase[i] = t * EDIM;
+            nkey[i] = t & 7;
         }
 #pragma unroll
         for (int s = 0; s < PD; ++s) {
@@ -224,18 +261,31 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
             v4i a[NTP];
 #pragma unroll
             for (int j = 0; j < NTP; ++j) a[j] = ring[s][j];
-            const int c = s * 2 + g;
-            v4i b[RT];
+            v4i bnxt[RT];
+            if (s + 1 < PD) {
+                const int c = (s + 1) * 2 + g;
 #pragma unroll
-            for (int i = 0; i < RT; ++i)
-                b[i] = *(const v4i *)(s_emb + ebase[i] + ((c ^ ekey[i]) << 4));
+                for (int i = 0; i < RT; ++i)
+                    bnxt[i] = *(const v4i *)(s_emb + ebase[i] + ((c ^ ekey[i]) << 4));
+            } else {
+#pragma unroll
+                for (int i = 0; i < RT; ++i)
+                    bnxt[i] = *(const v4i *)(s_emb + nbase[i] + ((g ^ nkey[i]) << 4));
+            }
 #pragma unroll
             for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], kt + PD);
 #pragma unroll
             for (int j = 0; j < NTP; ++j)
 #pragma unroll
                 for (int i = 0; i < RT; ++i)
-                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b[i], acc[j][i], 0, 0, 0);
+                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bcur[i], acc[j][i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) bcur[i] = bnxt[i];
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            ebase[i] = nbase[i];
+            ekey[i] = nkey[i];
         }
     }
 }
@@ -261,9 +311,16 @@ __device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const L
             for (int i = 0; i < RT; ++i) {
                 uint32_t packed = 0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    packed |= requant_u8(acc[j][i][4 * g + e], bb[e], (uint32_t)mm[e],
-                                         (ss >> (8 * e)) & 63u, lo) << (8 * e);
+                for (int e = 0; e < 4; ++e) {
+                    // read the accumulator out of its AGPR here, one at a
+                    // time (otherwise every accumulator is copied to VGPRs
+                    // at the end of the k loop, which spills)
+                    int a;
+                    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[j][i][4 * g + e]));
+                    const uint32_t sh = (ss >> (8 * e)) & 63u;
+                    packed |= (L.fast ? requant_u8_fast(a, bb[e], mm[e], sh, lo)
+                                      : requant_u8(a, bb[e], (uint32_t)mm[e], sh, lo)) << (8 * e);
+                }
                 // materialise the packed word here: without this the compiler
                 // sinks the requantisation below the next pass's GEMM and keeps
                 // every accumulator and parameter alive across it (spills)

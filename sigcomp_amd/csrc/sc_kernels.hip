@@ -20,7 +20,7 @@ namespace {
 
 constexpr int RT_TILE = 4;          // rows per MLP tile = 32 * RT_TILE = 128
 constexpr int R_TILE = 32 * RT_TILE;
-constexpr int DEC_RT_MAX = 4;       // decode: up to 128 chunks per workgroup
+constexpr int DEC_RT_MAX = 6;       // decode: up to 192 chunks per workgroup
 
 // ---- explicit context windows (GPUBitExactMLPDecoder._ar_step) ----------
 
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
-        mlp_rows<RT_TILE, 2>(M, s_emb, s_act, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+        mlp_rows<RT_TILE, 1>(M, s_emb, s_act, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
                           wave, lane);
         if (MODE == OUT_LOGITS) {
             // 128 rows x 256 bytes, 16-byte chunks, coalesced
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                 s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
             }
             __syncthreads();
-            mlp_rows<RT_TILE, 2>(M, s_emb, s_act, [&](int r, int p) { return (int)s_tok[r + p]; },
+            mlp_rows<RT_TILE, 1>(M, s_emb, s_act, [&](int r, int p) { return (int)s_tok[r + p]; },
                               wave, lane);
             const int32_t valid = min(R_TILE, L - t0);
             for (int r = wave; r < valid; r += WAVES) {
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __syncthreads();
     const int32_t maxlen = s_maxlen;
     for (int32_t t = 0; t < maxlen; ++t) {
-        mlp_rows<RT, 2>(M, s_emb, s_act,
+        mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act,
                      [&](int r, int p) {
                          return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
                      },
@@ -474,7 +474,7 @@ int upload(sc_model *m, const std::vector<T> &host, const T **out) {
 // lane l, W[nt*32 + l%32][kt*32 + (l/32)*16 .. +16].
 std::vector<int8_t> pack_weight(const int8_t *w, int n, int k) {
     const int NT = n / 32, KT = k / 32;
-    std::vector<int8_t> out((size_t)n * k + WEIGHT_PAD_FRAGS * 64 * 16, 0);
+    std::vector<int8_t> out((size_t)n * k, 0);
     for (int nt = 0; nt < NT; ++nt)
         for (int kt = 0; kt < KT; ++kt)
             for (int l = 0; l < 64; ++l)
@@ -552,12 +552,26 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         std::vector<int32_t> bias(L.bias, L.bias + L.n);
         rc = upload(m, bias, &D.bias);
         if (rc) break;
+        // Requant constants.  m0 == 2**31 is rewritten as (2**30, shift - 1)
+        // (the same product); layers whose every m0 < 2**31 and shift >= 32
+        // take the 32-bit high-product path (requant_u8_fast).
         std::vector<uint32_t> m0(L.n);
         std::vector<uint8_t> sh(L.n);
+        bool fast = true;
         for (int j = 0; j < L.n; ++j) {
-            m0[j] = (uint32_t)L.m0[j];
-            sh[j] = (uint8_t)L.shift[j];
+            int64_t mj = L.m0[j];
+            int32_t sj = L.shift[j];
+            if (mj == (int64_t(1) << 31) && sj >= 1) {
+                mj >>= 1;
+                sj -= 1;
+            }
+            m0[j] = (uint32_t)mj;
+            sh[j] = (uint8_t)sj;
+            fast = fast && mj < (int64_t(1) << 31) && sj >= 32;
         }
+        if (fast)
+            for (int j = 0; j < L.n; ++j) sh[j] = (uint8_t)(sh[j] - 32);
+        D.fast = fast ? 1 : 0;
         rc = upload(m, m0, &D.m0);
         if (rc) break;
         rc = upload(m, sh, &D.shift);
@@ -720,6 +734,8 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
         SC_DEC_CASE(2)
         SC_DEC_CASE(3)
         SC_DEC_CASE(4)
+        SC_DEC_CASE(5)
+        SC_DEC_CASE(6)
 #undef SC_DEC_CASE
     }
     return check_launch("k_decompress");
