@@ -36,11 +36,14 @@ constexpr int EMB_BYTES = EMB_ROWS * EDIM;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// Requant parameters of one 32-output n-tile, 72 dwords: bias[32] (int32),
+// m0[32] (uint32), shift[32] (uint8, packed four per dword).
+constexpr int PAR_DWORDS = 72;
+constexpr int PAR_LDS_DWORDS = 4 * PAR_DWORDS * 4;   // 4 waves x up to 4 n-tiles
+
 struct LayerDev {
     const v4i *w;            // packed weight fragments (pack order: pack_weight in sc_kernels.hip)
-    const int32_t *bias;     // [n]
-    const uint32_t *m0;      // [n]
-    const uint8_t *shift;    // [n]
+    const uint32_t *par;     // [n/32][PAR_DWORDS] requant parameter blocks
     int32_t n, kt;           // output width, k-tiles of 32
     int32_t relu;
     int32_t bytes;           // size of the packed weight buffer
@@ -169,123 +172,148 @@ __device__ __forceinline__ v4i wload(const WStream &ws, int voff, int kt) {
     return (v4i)x;
 }
 
+
+// Pin the instruction order of one k-step: the RT LDS reads of the next
+// step's B fragments and the NTP weight loads are spread between this
+// step's MFMAs, so their latency overlaps the MFMA pipeline.
+template <int NTP, int RT>
+__device__ __forceinline__ void kstep_schedule() {
+    constexpr int MF = NTP * RT;
+    constexpr int per = MF / (RT + NTP) > 0 ? MF / (RT + NTP) : 1;
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, per, 0); // MFMA
+    }
+#pragma unroll
+    for (int j = 0; j < NTP; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x008, per, 0); // MFMA
+    }
+    if constexpr (MF - per * (RT + NTP) > 0)
+        __builtin_amdgcn_sched_group_barrier(0x008, MF - per * (RT + NTP), 0);
+}
+
 // Hidden / output layer: B operand from the activation rows in LDS.
 // The wave computes output n-tiles [nt0, nt0 + NTP) for all RT row tiles.
-// B fragments are read one k-tile ahead of their MFMAs (the read for the
-// step past the end wraps to k-tile 0 and is unused).
+//
+// Software pipeline (per k-step): the B fragments of the next k-step are
+// read from LDS and the weight fragments PD k-steps ahead are loaded while
+// this step's MFMAs run.  Weights live in two register sets w[0], w[1] of PD
+// k-steps each and B in two buffers; the loop body covers 2*PD k-steps so
+// every register keeps one role across the back-edge (no copies that would
+// wait on in-flight loads).
 template <int NTP, int RT, int KT>
 __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const uint8_t *s_act,
                                             v16i (&acc)[NTP][RT], int lane) {
     constexpr int PD = 4;
-    static_assert(KT % PD == 0 && (KT & (KT - 1)) == 0, "k-tiles: power of two, multiple of PD");
+    static_assert(KT % (2 * PD) == 0 && (KT & (KT - 1)) == 0, "k-tiles: power of two, multiple of 2*PD");
     int voff[NTP];
 #pragma unroll
     for (int j = 0; j < NTP; ++j) voff[j] = (nt0 + j) * KT * 1024 + lane * 16;
-    v4i ring[PD][NTP];
+    v4i w[2][PD][NTP];
 #pragma unroll
     for (int s = 0; s < PD; ++s)
 #pragma unroll
-        for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], s);
+        for (int j = 0; j < NTP; ++j) w[0][s][j] = wload(ws, voff[j], s);
     const int rl = lane & 31, g = lane >> 5;
     int roff[RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) roff[i] = (i * 32 + rl) * ACT_ROW;
     const int key = rl & 15;   // act_off swizzle key; (i*32 + rl) & 15 == rl & 15
-    v4i bcur[RT];
+    v4i b[2][RT];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) bcur[i] = *(const v4i *)(s_act + roff[i] + ((g ^ key) << 4));
+    for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_act + roff[i] + ((g ^ key) << 4));
 #pragma unroll 1
-    for (int kt0 = 0; kt0 < KT; kt0 += PD) {
+    for (int kt0 = 0; kt0 < KT; kt0 += 2 * PD) {
 #pragma unroll
-        for (int s = 0; s < PD; ++s) {
+        for (int s = 0; s < 2 * PD; ++s) {
             const int kt = kt0 + s;
-            v4i a[NTP];
-#pragma unroll
-            for (int j = 0; j < NTP; ++j) a[j] = ring[s][j];
-            v4i bnxt[RT];
+            const int ws_cur = s / PD, ws_nxt = ws_cur ^ 1, slot = s % PD;
+            const int bc = s & 1, bn = bc ^ 1;
             const int cn = (((kt + 1) & (KT - 1)) * 2 + g) ^ key;
 #pragma unroll
-            for (int i = 0; i < RT; ++i) bnxt[i] = *(const v4i *)(s_act + roff[i] + (cn << 4));
+            for (int i = 0; i < RT; ++i) b[bn][i] = *(const v4i *)(s_act + roff[i] + (cn << 4));
 #pragma unroll
-            for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], kt + PD);
+            for (int j = 0; j < NTP; ++j) w[ws_nxt][slot][j] = wload(ws, voff[j], kt + PD);
 #pragma unroll
             for (int j = 0; j < NTP; ++j)
 #pragma unroll
                 for (int i = 0; i < RT; ++i)
-                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bcur[i], acc[j][i], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < RT; ++i) bcur[i] = bnxt[i];
+                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[ws_cur][slot][j], b[bc][i],
+                                                                      acc[j][i], 0, 0, 0);
+            kstep_schedule<NTP, RT>();
+            __builtin_amdgcn_sched_barrier(0);   // one scheduling region per k-step
         }
     }
 }
 
 // Layer 0: the B operand row r, k = p*128 + j is emb[tok(r, p)][j], gathered
-// from the LDS embedding table; a k-tile of 32 never straddles a position.
-// Tokens are looked up one position ahead and B fragments one k-tile ahead.
+// from the LDS embedding table; a k-tile of 32 never straddles a position,
+// so a position is PD = 4 k-steps.  Same pipeline as gemm_hidden over pairs
+// of positions; tokens are read two positions ahead and turned into table
+// addresses one position ahead.
 template <int NTP, int RT, class TokFn>
 __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
                                             TokFn tok, v16i (&acc)[NTP][RT], int lane) {
-    constexpr int PD = 4;   // = k-tiles per position, so one position per outer step
+    constexpr int PD = 4;
+    static_assert(WIN % 2 == 0, "positions are processed in pairs");
     int voff[NTP];
 #pragma unroll
     for (int j = 0; j < NTP; ++j) voff[j] = (nt0 + j) * KT0 * 1024 + lane * 16;
-    v4i ring[PD][NTP];
+    v4i w[2][PD][NTP];
 #pragma unroll
     for (int s = 0; s < PD; ++s)
 #pragma unroll
-        for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], s);
+        for (int j = 0; j < NTP; ++j) w[0][s][j] = wload(ws, voff[j], s);
     const int rl = lane & 31, g = lane >> 5;
-    int ebase[RT], ekey[RT];
+    // eb/ek[x]: table row offset and swizzle key of the position with parity x;
+    // tk[x]: raw tokens of the next unconverted position with parity x
+    int eb[2][RT], ek[2][RT], tk[2][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
         const int t = tok(i * 32 + rl, 0);
-        ebase[i] = t * EDIM;
-        ekey[i] = t & 7;
+        eb[0][i] = t * EDIM;
+        ek[0][i] = t & 7;
+        tk[1][i] = tok(i * 32 + rl, 1);
     }
-    v4i bcur[RT];
+    v4i b[2][RT];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) bcur[i] = *(const v4i *)(s_emb + ebase[i] + ((g ^ ekey[i]) << 4));
+    for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_emb + eb[0][i] + ((g ^ ek[0][i]) << 4));
 #pragma unroll 1
-    for (int p = 0; p < WIN; ++p) {
-        int nbase[RT], nkey[RT];
-        const int pn = p + 1 < WIN ? p + 1 : WIN - 1;
+    for (int p0 = 0; p0 < WIN; p0 += 2) {
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-            const int t = tok(i * 32 + rl, pn);
-            nbase[i] = t * EDIM;
-            nkey[i] = t & 7;
-        }
+        for (int h = 0; h < 2; ++h) {
+            const int p = p0 + h, hn = h ^ 1;
+            const int p2 = p + 2 < WIN ? p + 2 : WIN - 1;
 #pragma unroll
-        for (int s = 0; s < PD; ++s) {
-            const int kt = p * PD + s;
-            v4i a[NTP];
-#pragma unroll
-            for (int j = 0; j < NTP; ++j) a[j] = ring[s][j];
-            v4i bnxt[RT];
-            if (s + 1 < PD) {
-                const int c = (s + 1) * 2 + g;
-#pragma unroll
-                for (int i = 0; i < RT; ++i)
-                    bnxt[i] = *(const v4i *)(s_emb + ebase[i] + ((c ^ ekey[i]) << 4));
-            } else {
-#pragma unroll
-                for (int i = 0; i < RT; ++i)
-                    bnxt[i] = *(const v4i *)(s_emb + nbase[i] + ((g ^ nkey[i]) << 4));
+            for (int i = 0; i < RT; ++i) {
+                eb[hn][i] = tk[hn][i] * EDIM;      // position p + 1
+                ek[hn][i] = tk[hn][i] & 7;
+                tk[h][i] = tok(i * 32 + rl, p2);   // position p + 2
             }
 #pragma unroll
-            for (int j = 0; j < NTP; ++j) ring[s][j] = wload(ws, voff[j], kt + PD);
+            for (int s = 0; s < PD; ++s) {
+                const int kt = p * PD + s;
+                const int bc = s & 1, bn = bc ^ 1;
 #pragma unroll
-            for (int j = 0; j < NTP; ++j)
+                for (int i = 0; i < RT; ++i) {
+                    const int base = s + 1 < PD ? eb[h][i] : eb[hn][i];
+                    const int k2 = s + 1 < PD ? ek[h][i] : ek[hn][i];
+                    const int c = ((s + 1) % PD) * 2 + g;
+                    b[bn][i] = *(const v4i *)(s_emb + base + ((c ^ k2) << 4));
+                }
 #pragma unroll
-                for (int i = 0; i < RT; ++i)
-                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bcur[i], acc[j][i], 0, 0, 0);
+                for (int j = 0; j < NTP; ++j) w[hn][s][j] = wload(ws, voff[j], kt + PD);
 #pragma unroll
-            for (int i = 0; i < RT; ++i) bcur[i] = bnxt[i];
-        }
+                for (int j = 0; j < NTP; ++j)
 #pragma unroll
-        for (int i = 0; i < RT; ++i) {
-            ebase[i] = nbase[i];
-            ekey[i] = nkey[i];
+                    for (int i = 0; i < RT; ++i)
+                        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i], acc[j][i],
+                                                                          0, 0, 0);
+                kstep_schedule<NTP, RT>();
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 }
@@ -293,20 +321,27 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
 // Requantise accumulators to packed int8.  Accumulator element v of tile
 // (j, i) is output feature n = (nt0 + j)*32 + 8*(v/4) + 4*(lane/32) + v%4 of
 // row r = i*32 + lane%32, so pk[j][i][g] holds features n0 .. n0+3 with
-// n0 = (nt0 + j)*32 + 8*g + 4*(lane/32).
+// n0 = (nt0 + j)*32 + 8*g + 4*(lane/32).  `par` points at the LDS copy of
+// the parameter block of n-tile nt0.
 template <int NTP, int RT>
-__device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const LayerDev &L, int nt0,
-                                             int lane, uint32_t (&pk)[NTP][RT][4]) {
+__device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const LayerDev &L,
+                                             const uint32_t *par, int lane, uint32_t (&pk)[NTP][RT][4]) {
     const int g2 = lane >> 5;
     const int lo = L.relu ? 0 : -128;
 #pragma unroll
     for (int j = 0; j < NTP; ++j) {
+        const uint32_t *pj = par + j * PAR_DWORDS;
+        v4i bb[4], mm[4];
+        uint32_t ss[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int n0 = (nt0 + j) * 32 + 8 * g + 4 * g2;
-            const v4i bb = *(const v4i *)(L.bias + n0);
-            const v4i mm = *(const v4i *)(L.m0 + n0);
-            const uint32_t ss = *(const uint32_t *)(L.shift + n0);
+            const int o = 8 * g + 4 * g2;
+            bb[g] = *(const v4i *)(pj + o);
+            mm[g] = *(const v4i *)(pj + 32 + o);
+            ss[g] = pj[64 + (o >> 2)];
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
             for (int i = 0; i < RT; ++i) {
                 uint32_t packed = 0;
@@ -317,9 +352,9 @@ __device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const L
                     // at the end of the k loop, which spills)
                     int a;
                     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[j][i][4 * g + e]));
-                    const uint32_t sh = (ss >> (8 * e)) & 63u;
-                    packed |= (L.fast ? requant_u8_fast(a, bb[e], mm[e], sh, lo)
-                                      : requant_u8(a, bb[e], (uint32_t)mm[e], sh, lo)) << (8 * e);
+                    const uint32_t sh = (ss[g] >> (8 * e)) & 63u;
+                    packed |= (L.fast ? requant_u8_fast(a, bb[g][e], mm[g][e], sh, lo)
+                                      : requant_u8(a, bb[g][e], (uint32_t)mm[g][e], sh, lo)) << (8 * e);
                 }
                 // materialise the packed word here: without this the compiler
                 // sinks the requantisation below the next pass's GEMM and keeps
@@ -349,24 +384,43 @@ __device__ __forceinline__ void store_packed(const uint32_t (&pk)[NTP][RT][4], i
 // One layer over R = 32*RT rows.  Wave w owns n-tiles
 // [w*NTP*PASSES, (w+1)*NTP*PASSES), computed NTP at a time; the int8 results
 // of every pass are held in registers until all waves have finished reading
-// the layer input, then written over it.  Leaves with a barrier.
+// the layer input, then written over it.  The wave's requant parameter
+// blocks are loaded before its GEMM and copied to its LDS slot `s_par`
+// afterwards.  Leaves with a barrier.
 template <int NTP, int PASSES, int RT, bool FIRST, class TokFn>
 __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_emb, uint8_t *s_act,
-                                          TokFn tok, int wave, int lane) {
+                                          uint32_t *s_par, TokFn tok, int wave, int lane) {
+    constexpr int NTW = NTP * PASSES;                 // n-tiles per wave
+    constexpr int PW = NTW * PAR_DWORDS;              // parameter dwords per wave
+    constexpr int PL = (PW + 63) / 64;                // per lane
+    static_assert(NTW <= 4, "LDS parameter slot holds 4 n-tiles per wave");
+    const int ntw0 = wave * NTW;
+    uint32_t pr[PL];
+#pragma unroll
+    for (int d = 0; d < PL; ++d) {
+        const int idx = d * 64 + lane;
+        pr[d] = idx < PW ? L.par[ntw0 * PAR_DWORDS + idx] : 0u;
+    }
+    uint32_t *par = s_par + wave * 4 * PAR_DWORDS;
     uint32_t pk[PASSES][NTP][RT][4];
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass) {
-        const int nt0 = (wave * PASSES + pass) * NTP;
+        const int nt0 = ntw0 + pass * NTP;
         v16i acc[NTP][RT];
         zero_acc(acc);
         const WStream ws = make_wstream(L.w, L.bytes);
         if constexpr (FIRST) gemm_layer0<NTP, RT>(ws, nt0, s_emb, tok, acc, lane);
         else gemm_hidden<NTP, RT, KTH>(ws, nt0, s_act, acc, lane);
-        requant_pack(acc, L, nt0, lane, pk[pass]);
+        if (pass == 0) {
+#pragma unroll
+            for (int d = 0; d < PL; ++d)
+                if (d * 64 + lane < PW) par[d * 64 + lane] = pr[d];
+        }
+        requant_pack(acc, L, par + pass * NTP * PAR_DWORDS, lane, pk[pass]);
     }
     if constexpr (!FIRST) __syncthreads();
 #pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) store_packed(pk[pass], (wave * PASSES + pass) * NTP, s_act, lane);
+    for (int pass = 0; pass < PASSES; ++pass) store_packed(pk[pass], ntw0 + pass * NTP, s_act, lane);
     __syncthreads();
 }
 
@@ -376,14 +430,14 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
 // hidden layer (1: 4 n-tiles per pass; 2: 2 n-tiles per pass, fewer registers).
 template <int RT, int HP, class TokFn>
 __device__ __forceinline__ void mlp_rows(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
-                                         TokFn tok, int wave, int lane) {
+                                         uint32_t *s_par, TokFn tok, int wave, int lane) {
     static_assert(WAVES * 4 * 32 == HID && WAVES * 2 * 32 == VOCAB, "tile split assumes 4 waves");
     constexpr int HN = 4 / HP;
-    mlp_layer<HN, HP, RT, true>(M.layer[0], s_emb, s_act, tok, wave, lane);
+    mlp_layer<HN, HP, RT, true>(M.layer[0], s_emb, s_act, s_par, tok, wave, lane);
 #pragma unroll 1
     for (int l = 1; l < M.n_layers - 1; ++l)
-        mlp_layer<HN, HP, RT, false>(M.layer[l], s_emb, s_act, tok, wave, lane);
-    mlp_layer<2, 1, RT, false>(M.layer[M.n_layers - 1], s_emb, s_act, tok, wave, lane);
+        mlp_layer<HN, HP, RT, false>(M.layer[l], s_emb, s_act, s_par, tok, wave, lane);
+    mlp_layer<2, 1, RT, false>(M.layer[M.n_layers - 1], s_emb, s_act, s_par, tok, wave, lane);
 }
 
 // ---------------------------------------------------------------- frequencies
@@ -399,51 +453,123 @@ __device__ __forceinline__ uint64_t div_floor_est(uint64_t n, uint64_t d, double
     return q;
 }
 
-struct RowFreq {
-    uint32_t f[4];   // frequencies of symbols 4*lane .. 4*lane+3
-    uint32_t e[4];   // exclusive cumulative frequencies of the same symbols
+// DPP moves within 16-lane rows (gfx9 encodings): quad_perm xor 1 / xor 2,
+// row_half_mirror, row_mirror, row_shr:n.  Lanes whose source is outside
+// the row read 0.
+template <int CTRL>
+__device__ __forceinline__ int dpp(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+__device__ __forceinline__ int row16_max(int x) {
+    x = max(x, dpp<DPP_XOR1>(x));
+    x = max(x, dpp<DPP_XOR2>(x));
+    x = max(x, dpp<DPP_HALF_MIRROR>(x));
+    return max(x, dpp<DPP_MIRROR>(x));
+}
+__device__ __forceinline__ int row16_min(int x) {
+    x = min(x, dpp<DPP_XOR1>(x));
+    x = min(x, dpp<DPP_XOR2>(x));
+    x = min(x, dpp<DPP_HALF_MIRROR>(x));
+    return min(x, dpp<DPP_MIRROR>(x));
+}
+__device__ __forceinline__ uint32_t row16_sum(uint32_t x) {
+    x += (uint32_t)dpp<DPP_XOR1>((int)x);
+    x += (uint32_t)dpp<DPP_XOR2>((int)x);
+    x += (uint32_t)dpp<DPP_HALF_MIRROR>((int)x);
+    return x + (uint32_t)dpp<DPP_MIRROR>((int)x);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t x) {
+    const uint32_t lo = (uint32_t)dpp<CTRL>((int)(uint32_t)x);
+    const uint32_t hi = (uint32_t)dpp<CTRL>((int)(uint32_t)(x >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t row16_sum64(uint64_t x) {
+    x += dpp64<DPP_XOR1>(x);
+    x += dpp64<DPP_XOR2>(x);
+    x += dpp64<DPP_HALF_MIRROR>(x);
+    return x + dpp64<DPP_MIRROR>(x);
+}
+// exclusive prefix sum over the 16 lanes of a row
+__device__ __forceinline__ uint32_t row16_excl_scan(uint32_t x) {
+    uint32_t v = x;
+    v += (uint32_t)dpp<0x111>((int)v);   // row_shr:1
+    v += (uint32_t)dpp<0x112>((int)v);   // row_shr:2
+    v += (uint32_t)dpp<0x114>((int)v);   // row_shr:4
+    v += (uint32_t)dpp<0x118>((int)v);   // row_shr:8
+    return v - x;
+}
+
+// Frequency table of one row held by a 16-lane row of the wavefront: lane u
+// (= lane % 16) owns symbols 16u .. 16u+15.  f[k] = frequency of symbol
+// 16u+k, ex = exclusive cumulative frequency of symbol 16u.
+struct Freq16 {
+    uint32_t f[16];
+    uint32_t ex;
 };
 
-// cpu_entropy_coding.py:90-110 on one wavefront: lane holds logits of
-// symbols 4*lane .. 4*lane+3.  u = LUT[max - l]; T = sum u;
+// cpu_entropy_coding.py:90-110: u = LUT[max - l]; T = sum u;
 // f = max(u*2**24 // T, 1); the first argmax absorbs sum(f) - 2**24.
-__device__ __forceinline__ void row_frequencies(uint32_t packed_logits, const uint64_t *s_lut,
-                                                int lane, RowFreq &o) {
-    int l[4];
+__device__ __forceinline__ void row_frequencies16(v4i raw, const uint64_t *s_lut, int u, Freq16 &o) {
+    int l[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) l[i] = (int)(int8_t)(packed_logits >> (8 * i));
-    const int m = wave_max_i32(max(max(l[0], l[1]), max(l[2], l[3])));
-    uint64_t u[4];
+    for (int k = 0; k < 16; ++k) l[k] = (int)(int8_t)((uint32_t)raw[k >> 2] >> (8 * (k & 3)));
+    int lm = l[0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) u[i] = s_lut[m - l[i]];
-    const uint64_t T = wave_sum_u64(u[0] + u[1] + u[2] + u[3]);
-    const double rT = 1.0 / (double)T;
-    uint32_t f[4];
+    for (int k = 1; k < 16; ++k) lm = max(lm, l[k]);
+    const int m = row16_max(lm);
+    uint64_t uu[16];
+    uint64_t tl = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint64_t q = div_floor_est(u[i] << 24, T, rT);
-        f[i] = q < 1 ? 1u : (uint32_t)q;
+    for (int k = 0; k < 16; ++k) {
+        uu[k] = s_lut[m - l[k]];
+        tl += uu[k];
     }
-    const uint32_t S = wave_sum_u32(f[0] + f[1] + f[2] + f[3]);
-    const int fm = wave_max_i32((int)max(max(f[0], f[1]), max(f[2], f[3])));
+    const uint64_t T = row16_sum64(tl);
+    const double rT = 1.0 / (double)T;
+    uint32_t sl = 0, fl = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint64_t q = div_floor_est(uu[k] << 24, T, rT);
+        o.f[k] = q < 1 ? 1u : (uint32_t)q;
+        sl += o.f[k];
+        fl = max(fl, o.f[k]);
+    }
+    const uint32_t S = row16_sum(sl);
+    const int fm = row16_max((int)fl);
     int cand = 1 << 20;
 #pragma unroll
-    for (int i = 3; i >= 0; --i)
-        if ((int)f[i] == fm) cand = 4 * lane + i;
-    const int idx = wave_min_i32(cand);
-    if ((idx >> 2) == lane) {
+    for (int k = 15; k >= 0; --k)
+        if ((int)o.f[k] == fm) cand = 16 * u + k;
+    const int idx = row16_min(cand);
+    if ((idx >> 4) == u) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if ((idx & 3) == i) f[i] -= S - TOTAL;
+        for (int k = 0; k < 16; ++k)
+            if ((idx & 15) == k) o.f[k] -= S - TOTAL;
     }
-    const uint32_t tot = f[0] + f[1] + f[2] + f[3];
-    uint32_t ex = wave_incl_scan_u32(tot, lane) - tot;
+    uint32_t tot = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        o.f[i] = f[i];
-        o.e[i] = ex;
-        ex += f[i];
+    for (int k = 0; k < 16; ++k) tot += o.f[k];
+    o.ex = row16_excl_scan(tot);
+}
+
+// cumulative frequency and frequency of local symbol k (0..15) of this lane
+__device__ __forceinline__ void freq16_at(const Freq16 &fr, int k, uint32_t &cum, uint32_t &freq) {
+    uint32_t c = fr.ex, f = fr.f[0];
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+        if (x < k) c += fr.f[x];
+        if (x == k) f = fr.f[x];
     }
+    cum = c;
+    freq = f;
+}
+
+// logits of row r (in s_act) as the 16 bytes of lane u's symbols
+__device__ __forceinline__ v4i row_logits16(const uint8_t *s_act, int r, int u) {
+    return *(const v4i *)(s_act + act_off(r, u));
 }
 
 // ---------------------------------------------------------------- range coder
@@ -535,24 +661,26 @@ __device__ __forceinline__ bool dec_quantile(uint64_t D, uint64_t scale, uint32_
     return true;
 }
 
-// Symbol search on one wavefront: largest v with excl_cdf[v] <= q (the
+// Symbol search on a 16-lane row: largest v with excl_cdf[v] <= q (the
 // cumulative frequencies are strictly increasing since every f >= 1), as the
 // CPU loop (cpu_entropy_coding.py:251-254) and the Triton count
-// (gpu_entropy_coding.py:370-374).  Returns the symbol, its cum and freq.
-__device__ __forceinline__ int dec_symbol(const RowFreq &fr, uint32_t q, int lane,
-                                          uint32_t &cum, uint32_t &freq) {
-    uint32_t cnt = 0;
+// (gpu_entropy_coding.py:370-374).  All 16 lanes return the symbol and its
+// cum / freq.
+__device__ __forceinline__ int dec_symbol16(const Freq16 &fr, uint32_t q, int lane, uint32_t &cum,
+                                            uint32_t &freq) {
+    uint32_t cnt = 0, c = fr.ex;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cnt += fr.e[i] <= q ? 1u : 0u;
-    int s = (int)wave_sum_u32(cnt) - 1;
+    for (int k = 0; k < 16; ++k) {
+        cnt += c <= q ? 1u : 0u;
+        c += fr.f[k];
+    }
+    int s = (int)row16_sum(cnt) - 1;
     s = s < 0 ? 0 : (s > 255 ? 255 : s);
-    const int src = s >> 2, sel = s & 3;
-    uint32_t ce = fr.e[0], cf = fr.f[0];
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (sel == i) { ce = fr.e[i]; cf = fr.f[i]; }
-    cum = (uint32_t)__shfl((int)ce, src);
-    freq = (uint32_t)__shfl((int)cf, src);
+    uint32_t mc, mf;
+    freq16_at(fr, s & 15, mc, mf);
+    const int src = (lane & ~15) | (s >> 4);
+    cum = (uint32_t)__shfl((int)mc, src);
+    freq = (uint32_t)__shfl((int)mf, src);
     return s;
 }
 

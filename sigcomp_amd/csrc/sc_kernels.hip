@@ -22,6 +22,9 @@ constexpr int RT_TILE = 4;          // rows per MLP tile = 32 * RT_TILE = 128
 constexpr int R_TILE = 32 * RT_TILE;
 constexpr int DEC_RT_MAX = 6;       // decode: up to 192 chunks per workgroup
 
+// Rows of a tile are post-processed four at a time per wavefront: row
+// 4*gi + lane/16 is handled by the 16-lane row lane/16 (see Freq16).
+
 // ---- explicit context windows (GPUBitExactMLPDecoder._ar_step) ----------
 
 enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
@@ -34,8 +37,10 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
     __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
     __shared__ uint64_t s_lut[VOCAB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
     const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
@@ -54,8 +59,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
-        mlp_rows<RT_TILE, 1>(M, s_emb, s_act, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
-                          wave, lane);
+        mlp_rows<RT_TILE, 1>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+                             wave, lane);
         if (MODE == OUT_LOGITS) {
             // 128 rows x 256 bytes, 16-byte chunks, coalesced
             for (int i = threadIdx.x; i < R_TILE * 16; i += THREADS) {
@@ -64,15 +69,20 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
                     *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_off(r, c));
             }
         } else {
-            for (int r = wave; r < R_TILE; r += WAVES) {
-                if (row0 + r >= rows) break;
-                const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
-                RowFreq fr;
-                row_frequencies(pl, s_lut, lane, fr);
-                int32_t *dst = cdf + (row0 + r) * (VOCAB + 1);
+            for (int gi = wave; gi < R_TILE / 4; gi += WAVES) {
+                const int r = gi * 4 + q4;
+                Freq16 fr;
+                row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
+                if (row0 + r < rows) {
+                    int32_t *dst = cdf + (row0 + r) * (VOCAB + 1) + 16 * u;
+                    uint32_t c = fr.ex;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dst[4 * lane + i] = (int32_t)fr.e[i];
-                if (lane == 63) dst[VOCAB] = (int32_t)TOTAL;
+                    for (int k = 0; k < 16; ++k) {
+                        dst[k] = (int32_t)c;
+                        c += fr.f[k];
+                    }
+                    if (u == 15) dst[16] = (int32_t)TOTAL;
+                }
             }
         }
     }
@@ -90,10 +100,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                                                              unsigned int *__restrict__ counter) {
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ uint64_t s_lut[VOCAB];
     __shared__ int64_t s_unit;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
     for (;;) {
@@ -112,20 +124,18 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                 s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
             }
             __syncthreads();
-            mlp_rows<RT_TILE, 1>(M, s_emb, s_act, [&](int r, int p) { return (int)s_tok[r + p]; },
-                              wave, lane);
+            mlp_rows<RT_TILE, 1>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
+                                 wave, lane);
             const int32_t valid = min(R_TILE, L - t0);
-            for (int r = wave; r < valid; r += WAVES) {
-                const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
-                RowFreq fr;
-                row_frequencies(pl, s_lut, lane, fr);
+            for (int gi = wave; gi * 4 < valid; gi += WAVES) {
+                const int r = gi * 4 + q4;
+                Freq16 fr;
+                row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
                 const int s = s_tok[r + WIN];
-                if ((s >> 2) == lane) {
-                    uint32_t ce = fr.e[0], cf = fr.f[0];
-#pragma unroll
-                    for (int i = 1; i < 4; ++i)
-                        if ((s & 3) == i) { ce = fr.e[i]; cf = fr.f[i]; }
-                    out[t0 + r] = make_uint2(ce, cf);
+                if (r < valid && (s >> 4) == u) {
+                    uint32_t cum, freq;
+                    freq16_at(fr, s & 15, cum, freq);
+                    out[t0 + r] = make_uint2(cum, freq);
                 }
             }
             __syncthreads();
@@ -185,12 +195,14 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R * ACT_ROW];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
     __shared__ uint64_t s_lut[VOCAB];
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
     __shared__ int64_t s_woff[R], s_toff[R];
     __shared__ int32_t s_rpos[R], s_wcnt[R], s_len[R], s_stat[R];
     __shared__ int32_t s_maxlen;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * R;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
@@ -225,44 +237,47 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __syncthreads();
     const int32_t maxlen = s_maxlen;
     for (int32_t t = 0; t < maxlen; ++t) {
-        mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act,
+        mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par,
                      [&](int r, int p) {
                          return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
                      },
                      wave, lane);
-        for (int r = wave; r < R; r += WAVES) {
-            if (t >= s_len[r] || s_stat[r]) continue;
-            const uint32_t pl = *(const uint32_t *)(s_act + act_off(r, lane >> 2) + ((lane * 4) & 15));
-            RowFreq fr;
-            row_frequencies(pl, s_lut, lane, fr);
-            // _decode_partition (cpu_entropy_coding.py:230-266)
+        for (int gi = wave; gi < R / 4; gi += WAVES) {
+            const int r = gi * 4 + q4;
+            Freq16 fr;
+            row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
+            // _decode_partition (cpu_entropy_coding.py:230-266); the 16 lanes
+            // of the row compute the same state, lane u == 0 stores it
+            const bool active = t < s_len[r] && s_stat[r] == 0;
             uint64_t lower = s_lower[r], range = s_range[r], point = s_point[r];
             const uint64_t scale = range >> 24;
             uint32_t q = 0;
             const bool ok = scale != 0 && dec_quantile(point - lower, scale, q);
-            if (!ok) {
-                if (lane == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
-                continue;
-            }
             uint32_t cum, freq;
-            const int sym = dec_symbol(fr, q, lane, cum, freq);
-            lower += scale * cum;
-            range = scale * freq;
-            int32_t rpos = s_rpos[r];
-            if (range < (1ull << 32)) {
-                lower <<= 32;
-                range <<= 32;
-                point <<= 32;
-                if (rpos < s_wcnt[r]) point |= words[s_woff[r] + rpos];
-                rpos += 1;
-            }
-            if (lane == 0) {
-                s_lower[r] = lower;
-                s_range[r] = range;
-                s_point[r] = point;
-                s_rpos[r] = rpos;
-                s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
-                tokens[s_toff[r] + t] = (uint8_t)sym;
+            const int sym = dec_symbol16(fr, q, lane, cum, freq);
+            if (active) {
+                if (!ok) {
+                    if (u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
+                } else {
+                    lower += scale * cum;
+                    range = scale * freq;
+                    int32_t rpos = s_rpos[r];
+                    if (range < (1ull << 32)) {
+                        lower <<= 32;
+                        range <<= 32;
+                        point <<= 32;
+                        if (rpos < s_wcnt[r]) point |= words[s_woff[r] + rpos];
+                        rpos += 1;
+                    }
+                    if (u == 0) {
+                        s_lower[r] = lower;
+                        s_range[r] = range;
+                        s_point[r] = point;
+                        s_rpos[r] = rpos;
+                        s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
+                        tokens[s_toff[r] + t] = (uint8_t)sym;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -272,10 +287,15 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
 }
 
 // ---- step-API kernels (GpuRangeStepEncoder / GpuRangeDecoder) ------------
+// 256 threads = 16 rows per workgroup (four 16-lane rows per wavefront).
 
 __device__ __forceinline__ void stage_lut(const uint64_t *lut, uint64_t *s_lut) {
     for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = lut[i];
     __syncthreads();
+}
+
+__device__ __forceinline__ v4i global_logits16(const int8_t *logits, int64_t row, int64_t rows, int u) {
+    return row < rows ? *(const v4i *)(logits + row * VOCAB + 16 * u) : v4i{0, 0, 0, 0};
 }
 
 __global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict__ logits, int64_t rows,
@@ -283,15 +303,19 @@ __global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict_
                                                        int64_t *__restrict__ cdf) {
     __shared__ uint64_t s_lut[VOCAB];
     stage_lut(lut, s_lut);
-    const int lane = threadIdx.x & 63;
-    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int u = threadIdx.x & 15;
+    const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    Freq16 fr;
+    row_frequencies16(global_logits16(logits, r, rows, u), s_lut, u, fr);
     if (r >= rows) return;
-    RowFreq fr;
-    row_frequencies(*(const uint32_t *)(logits + r * VOCAB + 4 * lane), s_lut, lane, fr);
-    int64_t *dst = cdf + r * (VOCAB + 1);
+    int64_t *dst = cdf + r * (VOCAB + 1) + 16 * u;
+    uint32_t c = fr.ex;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[4 * lane + i] = fr.e[i];
-    if (lane == 63) dst[VOCAB] = TOTAL;
+    for (int k = 0; k < 16; ++k) {
+        dst[k] = c;
+        c += fr.f[k];
+    }
+    if (u == 15) dst[16] = TOTAL;
 }
 
 struct EncArrays {
@@ -309,35 +333,30 @@ __global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ 
                                                      int64_t max_words) {
     __shared__ uint64_t s_lut[VOCAB];
     stage_lut(lut, s_lut);
-    const int lane = threadIdx.x & 63;
-    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int u = threadIdx.x & 15;
+    const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    Freq16 fr;
+    row_frequencies16(global_logits16(logits, b, B, u), s_lut, u, fr);
     if (b >= B || t >= valid[b] || st.status[b]) return;
     const int64_t sym = symbols[b];
     if (sym < 0 || sym >= VOCAB) {
-        if (lane == 0) st.status[b] = SC_STATUS_BAD_TOKEN;
+        if (u == 0) st.status[b] = SC_STATUS_BAD_TOKEN;
         return;
     }
-    RowFreq fr;
-    row_frequencies(*(const uint32_t *)(logits + b * VOCAB + 4 * lane), s_lut, lane, fr);
     const int s = (int)sym;
-    const uint32_t cum = (uint32_t)__shfl((int)(s & 3) == 0 ? (int)fr.e[0] : (s & 3) == 1 ? (int)fr.e[1]
-                                                          : (s & 3) == 2 ? (int)fr.e[2] : (int)fr.e[3],
-                                          s >> 2);
-    const uint32_t freq = (uint32_t)__shfl((int)(s & 3) == 0 ? (int)fr.f[0] : (s & 3) == 1 ? (int)fr.f[1]
-                                                           : (s & 3) == 2 ? (int)fr.f[2] : (int)fr.f[3],
-                                           s >> 2);
-    if (lane == 0) {
-        EncState e{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
-        if (enc_step(e, cum, freq, words + b * max_words, (int32_t)max_words)) {
-            st.status[b] = SC_STATUS_CAPACITY;
-            return;
-        }
-        st.lower[b] = e.lower;
-        st.range[b] = e.range;
-        st.inverted[b] = e.inverted;
-        st.first[b] = e.first;
-        st.write_pos[b] = e.pos;
+    if ((s >> 4) != u) return;   // the lane holding the symbol runs the coder
+    uint32_t cum, freq;
+    freq16_at(fr, s & 15, cum, freq);
+    EncState e{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
+    if (enc_step(e, cum, freq, words + b * max_words, (int32_t)max_words)) {
+        st.status[b] = SC_STATUS_CAPACITY;
+        return;
     }
+    st.lower[b] = e.lower;
+    st.range[b] = e.range;
+    st.inverted[b] = e.inverted;
+    st.first[b] = e.first;
+    st.write_pos[b] = e.pos;
 }
 
 __global__ __launch_bounds__(256) void k_encode_seal(int64_t B, EncArrays st, uint32_t *__restrict__ words,
@@ -370,27 +389,33 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
                                                      int64_t *__restrict__ symbols_out) {
     __shared__ uint64_t s_lut[VOCAB];
     stage_lut(lut, s_lut);
-    const int lane = threadIdx.x & 63;
-    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= B) return;
-    if (t >= valid[b] || st.status[b]) {
-        if (lane == 0) symbols_out[b] = VOCAB;
-        return;
+    const int lane = threadIdx.x & 63, u = threadIdx.x & 15;
+    const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    Freq16 fr;
+    row_frequencies16(global_logits16(logits, b, B, u), s_lut, u, fr);
+    const bool in_range = b < B;
+    const bool active = in_range && t < valid[b] && st.status[b] == 0;
+    uint64_t lower = 0, range = ~0ull, point = 0;
+    if (active) {
+        lower = st.lower[b];
+        range = st.range[b];
+        point = st.point[b];
     }
-    uint64_t lower = st.lower[b], range = st.range[b], point = st.point[b];
     const uint64_t scale = range >> 24;
     uint32_t q = 0;
-    if (scale == 0 || !dec_quantile(point - lower, scale, q)) {
-        if (lane == 0) {
-            st.status[b] = SC_STATUS_INVALID_STREAM;
-            symbols_out[b] = VOCAB;
-        }
+    const bool ok = scale != 0 && dec_quantile(point - lower, scale, q);
+    uint32_t cum, freq;
+    const int sym = dec_symbol16(fr, q, lane, cum, freq);
+    if (!in_range || u != 0) return;
+    if (!active) {
+        symbols_out[b] = VOCAB;
         return;
     }
-    RowFreq fr;
-    row_frequencies(*(const uint32_t *)(logits + b * VOCAB + 4 * lane), s_lut, lane, fr);
-    uint32_t cum, freq;
-    const int sym = dec_symbol(fr, q, lane, cum, freq);
+    if (!ok) {
+        st.status[b] = SC_STATUS_INVALID_STREAM;
+        symbols_out[b] = VOCAB;
+        return;
+    }
     lower += scale * cum;
     range = scale * freq;
     int64_t rp = st.read_pos[b];
@@ -401,13 +426,11 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
         if (rp < st.end_pos[b]) point |= words[rp];
         rp += 1;
     }
-    if (lane == 0) {
-        st.lower[b] = lower;
-        st.range[b] = range;
-        st.point[b] = point;
-        st.read_pos[b] = rp;
-        symbols_out[b] = sym;
-    }
+    st.lower[b] = lower;
+    st.range[b] = range;
+    st.point[b] = point;
+    st.read_pos[b] = rp;
+    symbols_out[b] = sym;
 }
 
 }  // namespace
@@ -549,12 +572,11 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         rc = upload(m, packed, &wdev);
         D.w = (const v4i *)wdev;
         if (rc) break;
-        std::vector<int32_t> bias(L.bias, L.bias + L.n);
-        rc = upload(m, bias, &D.bias);
-        if (rc) break;
         // Requant constants.  m0 == 2**31 is rewritten as (2**30, shift - 1)
         // (the same product); layers whose every m0 < 2**31 and shift >= 32
-        // take the 32-bit high-product path (requant_u8_fast).
+        // take the 32-bit high-product path (requant_u8_fast), with
+        // shift - 32 stored.  Packed per 32-output n-tile: bias[32], m0[32],
+        // shift[32] (bytes), PAR_DWORDS dwords per n-tile.
         std::vector<uint32_t> m0(L.n);
         std::vector<uint8_t> sh(L.n);
         bool fast = true;
@@ -572,9 +594,18 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         if (fast)
             for (int j = 0; j < L.n; ++j) sh[j] = (uint8_t)(sh[j] - 32);
         D.fast = fast ? 1 : 0;
-        rc = upload(m, m0, &D.m0);
+        std::vector<uint32_t> par((size_t)(L.n / 32) * PAR_DWORDS, 0u);
+        for (int nt = 0; nt < L.n / 32; ++nt) {
+            uint32_t *blk = par.data() + (size_t)nt * PAR_DWORDS;
+            for (int x = 0; x < 32; ++x) {
+                const int j = nt * 32 + x;
+                blk[x] = (uint32_t)L.bias[j];
+                blk[32 + x] = m0[j];
+                blk[64 + x / 4] |= (uint32_t)sh[j] << (8 * (x % 4));
+            }
+        }
+        rc = upload(m, par, &D.par);
         if (rc) break;
-        rc = upload(m, sh, &D.shift);
         D.n = L.n;
         D.kt = L.k / 32;
         D.relu = L.relu ? 1 : 0;
@@ -631,7 +662,7 @@ int sc_logits_to_cdf(const int8_t *logits, int64_t rows, const uint64_t *lut, in
     if (rows < 0) return fail(SC_ERR_ARG, "rows must be nonnegative");
     if (rows == 0) return SC_OK;
     if (!logits || !lut || !cdf) return fail(SC_ERR_ARG, "null device pointer");
-    hipLaunchKernelGGL(k_logits_to_cdf, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, as_stream(stream),
+    hipLaunchKernelGGL(k_logits_to_cdf, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, as_stream(stream),
                        logits, rows, lut, cdf);
     return check_launch("k_logits_to_cdf");
 }
@@ -648,7 +679,7 @@ int sc_encode_step(const int8_t *logits, const uint64_t *lut, const int64_t *sym
     if (!logits || !lut || !symbols || !valid_lens || !words || !enc_ok(state))
         return fail(SC_ERR_ARG, "null device pointer");
     EncArrays a{state->lower, state->range, state->inverted, state->first, state->write_pos, state->status};
-    hipLaunchKernelGGL(k_encode_step, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, as_stream(stream), logits, lut,
+    hipLaunchKernelGGL(k_encode_step, dim3((unsigned)((B + 15) / 16)), dim3(256), 0, as_stream(stream), logits, lut,
                        symbols, valid_lens, t, B, a, words, max_words);
     return check_launch("k_encode_step");
 }
@@ -671,7 +702,7 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
         !state->point || !state->read_pos || !state->end_pos || !state->status || !words)
         return fail(SC_ERR_ARG, "null device pointer");
     DecArrays a{state->lower, state->range, state->point, state->read_pos, state->end_pos, state->status};
-    hipLaunchKernelGGL(k_decode_step, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, as_stream(stream), logits, lut,
+    hipLaunchKernelGGL(k_decode_step, dim3((unsigned)((B + 15) / 16)), dim3(256), 0, as_stream(stream), logits, lut,
                        valid_lens, t, B, a, words, symbols_out);
     return check_launch("k_decode_step");
 }
