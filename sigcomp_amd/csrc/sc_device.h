@@ -136,10 +136,8 @@ __device__ __forceinline__ uint32_t requant_u8(int acc, int bias, uint32_t m0, u
 __device__ __forceinline__ uint32_t requant_u8_fast(int acc, int bias, int m0, uint32_t shift32,
                                                     int lo) {
     const int biased = (int)((uint32_t)acc + (uint32_t)bias);
-    int s = __mulhi(biased, m0) >> shift32;
-    s = s < lo ? lo : s;
-    s = s > 127 ? 127 : s;
-    return (uint32_t)(uint8_t)(int8_t)s;
+    const int s = __mulhi(biased, m0) >> shift32;
+    return (uint32_t)(uint8_t)(int8_t)min(max(s, lo), 127);
 }
 
 // ---------------------------------------------------------------- MFMA GEMMs
@@ -323,22 +321,24 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
 // row r = i*32 + lane%32, so pk[j][i][g] holds features n0 .. n0+3 with
 // n0 = (nt0 + j)*32 + 8*g + 4*(lane/32).  `par` points at the LDS copy of
 // the parameter block of n-tile nt0.
-template <int NTP, int RT>
-__device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const LayerDev &L,
-                                             const uint32_t *par, int lane, uint32_t (&pk)[NTP][RT][4]) {
+template <int NTP, int RT, bool FAST, bool RELU>
+__device__ __forceinline__ void requant_pack_t(const v16i (&acc)[NTP][RT], const uint32_t *par, int lane,
+                                               uint32_t (&pk)[NTP][RT][4]) {
     const int g2 = lane >> 5;
-    const int lo = L.relu ? 0 : -128;
+    constexpr int lo = RELU ? 0 : -128;
 #pragma unroll
     for (int j = 0; j < NTP; ++j) {
         const uint32_t *pj = par + j * PAR_DWORDS;
         v4i bb[4], mm[4];
-        uint32_t ss[4];
+        uint32_t sh[4][4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int o = 8 * g + 4 * g2;
             bb[g] = *(const v4i *)(pj + o);
             mm[g] = *(const v4i *)(pj + 32 + o);
-            ss[g] = pj[64 + (o >> 2)];
+            const uint32_t ss = pj[64 + (o >> 2)];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sh[g][e] = (ss >> (8 * e)) & 63u;
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -352,9 +352,9 @@ __device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const L
                     // at the end of the k loop, which spills)
                     int a;
                     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[j][i][4 * g + e]));
-                    const uint32_t sh = (ss[g] >> (8 * e)) & 63u;
-                    packed |= (L.fast ? requant_u8_fast(a, bb[g][e], mm[g][e], sh, lo)
-                                      : requant_u8(a, bb[g][e], (uint32_t)mm[g][e], sh, lo)) << (8 * e);
+                    const uint32_t q = FAST ? requant_u8_fast(a, bb[g][e], mm[g][e], sh[g][e], lo)
+                                            : requant_u8(a, bb[g][e], (uint32_t)mm[g][e], sh[g][e], lo);
+                    packed |= q << (8 * e);
                 }
                 // materialise the packed word here: without this the compiler
                 // sinks the requantisation below the next pass's GEMM and keeps
@@ -366,6 +366,20 @@ __device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const L
     }
 }
 
+// One uniform branch per layer selects the requantisation variant.
+template <int NTP, int RT>
+__device__ __forceinline__ void requant_pack(const v16i (&acc)[NTP][RT], const LayerDev &L,
+                                             const uint32_t *par, int lane, uint32_t (&pk)[NTP][RT][4]) {
+    if (L.fast) {
+        if (L.relu) requant_pack_t<NTP, RT, true, true>(acc, par, lane, pk);
+        else requant_pack_t<NTP, RT, true, false>(acc, par, lane, pk);
+    } else {
+        if (L.relu) requant_pack_t<NTP, RT, false, true>(acc, par, lane, pk);
+        else requant_pack_t<NTP, RT, false, false>(acc, par, lane, pk);
+    }
+}
+
+// Natural feature order: pk[j][i][g] -> bytes n0 .. n0+3 of row r.
 template <int NTP, int RT>
 __device__ __forceinline__ void store_packed(const uint32_t (&pk)[NTP][RT][4], int nt0, uint8_t *s_act,
                                              int lane) {
@@ -381,13 +395,30 @@ __device__ __forceinline__ void store_packed(const uint32_t (&pk)[NTP][RT][4], i
         }
 }
 
+// Hidden-layer order: within each 32-feature block, feature 8g + 4h + e is
+// stored at byte 16h + 4g + e, so a lane's 16 results of one tile row form
+// one 16-byte chunk (one ds_write_b128).  The next layer's weight columns
+// are packed in the same order (pack_weight), so the products are unchanged.
+template <int NTP, int RT>
+__device__ __forceinline__ void store_packed_perm(const uint32_t (&pk)[NTP][RT][4], int nt0,
+                                                  uint8_t *s_act, int lane) {
+    const int rl = lane & 31, g2 = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < NTP; ++j)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            const v4i v = {(int)pk[j][i][0], (int)pk[j][i][1], (int)pk[j][i][2], (int)pk[j][i][3]};
+            *(v4i *)(s_act + act_off(i * 32 + rl, (nt0 + j) * 2 + g2)) = v;
+        }
+}
+
 // One layer over R = 32*RT rows.  Wave w owns n-tiles
 // [w*NTP*PASSES, (w+1)*NTP*PASSES), computed NTP at a time; the int8 results
 // of every pass are held in registers until all waves have finished reading
 // the layer input, then written over it.  The wave's requant parameter
 // blocks are loaded before its GEMM and copied to its LDS slot `s_par`
 // afterwards.  Leaves with a barrier.
-template <int NTP, int PASSES, int RT, bool FIRST, class TokFn>
+template <int NTP, int PASSES, int RT, bool FIRST, bool LAST, class TokFn>
 __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_emb, uint8_t *s_act,
                                           uint32_t *s_par, TokFn tok, int wave, int lane) {
     constexpr int NTW = NTP * PASSES;                 // n-tiles per wave
@@ -420,12 +451,16 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
     }
     if constexpr (!FIRST) __syncthreads();
 #pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) store_packed(pk[pass], ntw0 + pass * NTP, s_act, lane);
+    for (int pass = 0; pass < PASSES; ++pass) {
+        if constexpr (LAST) store_packed(pk[pass], ntw0 + pass * NTP, s_act, lane);
+        else store_packed_perm(pk[pass], ntw0 + pass * NTP, s_act, lane);
+    }
     __syncthreads();
 }
 
 // One MLP evaluation of R = 32*RT rows: tokens -> int8 logits in s_act rows
-// (bytes 0..255 of each row, same swizzle).  Must be entered after a barrier
+// (bytes 0..255 of each row in natural symbol order, same swizzle; hidden
+// activations use the store_packed_perm order).  Must be entered after a barrier
 // that ends every read of s_act; leaves with a barrier.  HP = passes per
 // hidden layer (1: 4 n-tiles per pass; 2: 2 n-tiles per pass, fewer registers).
 template <int RT, int HP, class TokFn>
@@ -433,11 +468,11 @@ __device__ __forceinline__ void mlp_rows(const ModelDev &M, const uint8_t *s_emb
                                          uint32_t *s_par, TokFn tok, int wave, int lane) {
     static_assert(WAVES * 4 * 32 == HID && WAVES * 2 * 32 == VOCAB, "tile split assumes 4 waves");
     constexpr int HN = 4 / HP;
-    mlp_layer<HN, HP, RT, true>(M.layer[0], s_emb, s_act, s_par, tok, wave, lane);
+    mlp_layer<HN, HP, RT, true, false>(M.layer[0], s_emb, s_act, s_par, tok, wave, lane);
 #pragma unroll 1
     for (int l = 1; l < M.n_layers - 1; ++l)
-        mlp_layer<HN, HP, RT, false>(M.layer[l], s_emb, s_act, s_par, tok, wave, lane);
-    mlp_layer<2, 1, RT, false>(M.layer[M.n_layers - 1], s_emb, s_act, s_par, tok, wave, lane);
+        mlp_layer<HN, HP, RT, false, false>(M.layer[l], s_emb, s_act, s_par, tok, wave, lane);
+    mlp_layer<2, 1, RT, false, true>(M.layer[M.n_layers - 1], s_emb, s_act, s_par, tok, wave, lane);
 }
 
 // ---------------------------------------------------------------- frequencies

@@ -494,16 +494,22 @@ int upload(sc_model *m, const std::vector<T> &host, const T **out) {
 }
 
 // Pack W [n, k] into MFMA A-operand fragments: fragment (nt, kt) holds, for
-// lane l, W[nt*32 + l%32][kt*32 + (l/32)*16 .. +16].
-std::vector<int8_t> pack_weight(const int8_t *w, int n, int k) {
+// lane l, the 16 weights of row nt*32 + l%32 at stored k positions
+// kt*32 + (l/32)*16 .. +16.  For layers fed by a hidden layer (perm_k) the
+// stored position p of a 32-column block holds column 8*((p%16)/4) +
+// 4*(p/16) + p%4, the order in which store_packed_perm lays out activations.
+std::vector<int8_t> pack_weight(const int8_t *w, int n, int k, bool perm_k) {
     const int NT = n / 32, KT = k / 32;
     std::vector<int8_t> out((size_t)n * k, 0);
     for (int nt = 0; nt < NT; ++nt)
         for (int kt = 0; kt < KT; ++kt)
             for (int l = 0; l < 64; ++l)
-                for (int b = 0; b < 16; ++b)
+                for (int b = 0; b < 16; ++b) {
+                    const int p = (l >> 5) * 16 + b;   // stored position within the block
+                    const int col = perm_k ? 8 * ((p & 15) >> 2) + 4 * (p >> 4) + (p & 3) : p;
                     out[(((size_t)nt * KT + kt) * 64 + l) * 16 + b] =
-                        w[(size_t)(nt * 32 + (l & 31)) * k + kt * 32 + (l >> 5) * 16 + b];
+                        w[(size_t)(nt * 32 + (l & 31)) * k + kt * 32 + col];
+                }
     return out;
 }
 
@@ -567,7 +573,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     for (int i = 0; i < n_layers && rc == SC_OK; ++i) {
         const sc_layer_desc &L = layers[i];
         LayerDev &D = m->dev.layer[i];
-        std::vector<int8_t> packed = pack_weight(L.weight, L.n, L.k);
+        std::vector<int8_t> packed = pack_weight(L.weight, L.n, L.k, i > 0);
         const int8_t *wdev = nullptr;
         rc = upload(m, packed, &wdev);
         D.w = (const v4i *)wdev;
