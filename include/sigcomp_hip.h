@@ -171,7 +171,9 @@ int sc_compress_chunks(const sc_model *model, const uint8_t *tokens, const int64
  * fused frequency step and decoder step per token, context kept on chip).
  * Chunk c: word_cnt[c] words at words + word_off[c] -> lengths[c] tokens at
  * tokens + tok_off[c]; status[c] is written (SC_STATUS_INVALID_STREAM on a
- * corrupt stream).  All arrays device.  Replaces
+ * corrupt stream).  All arrays device.  Chunks sorted by descending length
+ * (as QuantMLPCompression passes them) give the shortest schedule: the
+ * shortest chunks then land in the final, partial launch.  Replaces
  * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
  * (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */

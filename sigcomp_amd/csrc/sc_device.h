@@ -80,8 +80,9 @@ __device__ __forceinline__ void load_emb_lds(const int8_t *__restrict__ emb, uin
     }
 }
 
-__device__ __forceinline__ void load_lut_lds(const uint64_t *__restrict__ lut, uint64_t *s_lut) {
-    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = lut[i];
+// The exp-LUT is staged in LDS as float64 (entries <= 2**38 are exact).
+__device__ __forceinline__ void load_lut_lds(const uint64_t *__restrict__ lut, double *s_lut) {
+    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = (double)lut[i];
 }
 
 // ---------------------------------------------------------------- wave primitives
@@ -545,9 +546,27 @@ struct Freq16 {
     uint32_t ex;
 };
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+    return __builtin_bit_cast(double, dpp64<CTRL>(__builtin_bit_cast(uint64_t, x)));
+}
+__device__ __forceinline__ double row16_sum_f64(double x) {
+    x += dpp_f64<DPP_XOR1>(x);
+    x += dpp_f64<DPP_XOR2>(x);
+    x += dpp_f64<DPP_HALF_MIRROR>(x);
+    return x + dpp_f64<DPP_MIRROR>(x);
+}
+
 // cpu_entropy_coding.py:90-110: u = LUT[max - l]; T = sum u;
 // f = max(u*2**24 // T, 1); the first argmax absorbs sum(f) - 2**24.
-__device__ __forceinline__ void row_frequencies16(v4i raw, const uint64_t *s_lut, int u, Freq16 &o) {
+//
+// s_lut holds the LUT as float64 (every entry <= 2**38 is exact), so u and
+// every partial sum of T (integers < 2**53) are exact.  q = u * (2**24 / T)
+// is within 2**-28 of the true quotient (two roundings of relative 2**-53,
+// quotients <= 2**24), so floor(q) is exact unless q lies within 2**-20 of
+// an integer; a row with such a value redoes its 16 quotients with the
+// exact integer division (div_floor_est).
+__device__ __forceinline__ void row_frequencies16(v4i raw, const double *s_lut, int u, Freq16 &o) {
     int l[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) l[k] = (int)(int8_t)((uint32_t)raw[k >> 2] >> (8 * (k & 3)));
@@ -555,20 +574,36 @@ __device__ __forceinline__ void row_frequencies16(v4i raw, const uint64_t *s_lut
 #pragma unroll
     for (int k = 1; k < 16; ++k) lm = max(lm, l[k]);
     const int m = row16_max(lm);
-    uint64_t uu[16];
-    uint64_t tl = 0;
+    double uu[16];
+    double tl = 0.0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
         uu[k] = s_lut[m - l[k]];
         tl += uu[k];
     }
-    const uint64_t T = row16_sum64(tl);
-    const double rT = 1.0 / (double)T;
+    const double T = row16_sum_f64(tl);
+    const double r24 = 16777216.0 / T;
+    bool near = false;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const double q = uu[k] * r24;
+        const double fr = q - __builtin_floor(q);
+        near = near || fr < 0x1p-20 || fr > 1.0 - 0x1p-20;
+        const uint32_t fq = (uint32_t)q;
+        o.f[k] = fq < 1u ? 1u : fq;
+    }
+    if (near) {
+        const uint64_t Ti = (uint64_t)T;
+        const double rT = 1.0 / T;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint64_t q = div_floor_est(((uint64_t)uu[k]) << 24, Ti, rT);
+            o.f[k] = q < 1 ? 1u : (uint32_t)q;
+        }
+    }
     uint32_t sl = 0, fl = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        const uint64_t q = div_floor_est(uu[k] << 24, T, rT);
-        o.f[k] = q < 1 ? 1u : (uint32_t)q;
         sl += o.f[k];
         fl = max(fl, o.f[k]);
     }

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
     __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
     __shared__ uint16_t s_tok[R_TILE + WIN];
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     __shared__ int64_t s_unit;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R * ACT_ROW];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
     __shared__ int64_t s_woff[R], s_toff[R];
     __shared__ int32_t s_rpos[R], s_wcnt[R], s_len[R], s_stat[R];
@@ -289,8 +289,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
 // ---- step-API kernels (GpuRangeStepEncoder / GpuRangeDecoder) ------------
 // 256 threads = 16 rows per workgroup (four 16-lane rows per wavefront).
 
-__device__ __forceinline__ void stage_lut(const uint64_t *lut, uint64_t *s_lut) {
-    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = lut[i];
+__device__ __forceinline__ void stage_lut(const uint64_t *lut, double *s_lut) {
+    load_lut_lds(lut, s_lut);
     __syncthreads();
 }
 
@@ -301,7 +301,7 @@ __device__ __forceinline__ v4i global_logits16(const int8_t *logits, int64_t row
 __global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict__ logits, int64_t rows,
                                                        const uint64_t *__restrict__ lut,
                                                        int64_t *__restrict__ cdf) {
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     stage_lut(lut, s_lut);
     const int u = threadIdx.x & 15;
     const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ 
                                                      const int64_t *__restrict__ valid, int64_t t,
                                                      int64_t B, EncArrays st, uint32_t *__restrict__ words,
                                                      int64_t max_words) {
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     stage_lut(lut, s_lut);
     const int u = threadIdx.x & 15;
     const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
                                                      int64_t B, DecArrays st,
                                                      const uint32_t *__restrict__ words,
                                                      int64_t *__restrict__ symbols_out) {
-    __shared__ uint64_t s_lut[VOCAB];
+    __shared__ double s_lut[VOCAB];
     stage_lut(lut, s_lut);
     const int lane = threadIdx.x & 63, u = threadIdx.x & 15;
     const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -754,28 +754,51 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     if (!words || !word_off || !word_cnt || !lengths || !tokens || !tok_off || !status)
         return fail(SC_ERR_ARG, "null device pointer");
     DeviceGuard guard(m->device);
-    // rows per workgroup: enough 32-row tiles that one wave of workgroups
-    // covers every chunk, at most DEC_RT_MAX tiles
-    int64_t rt = (n_chunks + 32LL * m->n_cu - 1) / (32LL * m->n_cu);
-    rt = std::max<int64_t>(1, std::min<int64_t>(rt, DEC_RT_MAX));
-    const int64_t R = 32 * rt;
-    const unsigned grid = (unsigned)((n_chunks + R - 1) / R);
     hipStream_t s = as_stream(stream);
-    switch (rt) {
-#define SC_DEC_CASE(N)                                                                                         \
-    case N:                                                                                                    \
-        hipLaunchKernelGGL(k_decompress<N>, dim3(grid), dim3(THREADS), 0, s, m->dev, words, word_off, word_cnt, \
-                           lengths, n_chunks, tokens, tok_off, status);                                        \
+    // Launch plan.  A workgroup owns 32*rt consecutive chunks for the whole
+    // decode, one workgroup per CU.  Each launch is one full wave of n_cu
+    // workgroups at the largest rt that fills it (rt <= DEC_RT_MAX); the
+    // chunks left over (fewer than 32*n_cu) go to a final launch of rt = 1
+    // workgroups.  With chunks sorted longest first, the leftover launch
+    // holds the shortest chunks and ends quickly.
+    const int64_t cu = m->n_cu;
+    int64_t start = 0;
+    while (start < n_chunks) {
+        const int64_t left = n_chunks - start;
+        int64_t rt = std::min<int64_t>(left / (32 * cu), DEC_RT_MAX);
+        int64_t count;
+        unsigned grid;
+        if (rt >= 1) {
+            count = cu * 32 * rt;
+            grid = (unsigned)cu;
+        } else {
+            rt = 1;
+            count = left;
+            grid = (unsigned)((left + 31) / 32);
+        }
+        const uint32_t *wds = words;
+        const int64_t *woff = word_off + start, *toff = tok_off + start;
+        const int32_t *wcnt = word_cnt + start, *len = lengths + start;
+        int32_t *st = status + start;
+        switch (rt) {
+#define SC_DEC_CASE(N)                                                                                        \
+    case N:                                                                                                   \
+        hipLaunchKernelGGL(k_decompress<N>, dim3(grid), dim3(THREADS), 0, s, m->dev, wds, woff, wcnt, len,     \
+                           count, tokens, toff, st);                                                          \
         break;
-        SC_DEC_CASE(1)
-        SC_DEC_CASE(2)
-        SC_DEC_CASE(3)
-        SC_DEC_CASE(4)
-        SC_DEC_CASE(5)
-        SC_DEC_CASE(6)
+            SC_DEC_CASE(1)
+            SC_DEC_CASE(2)
+            SC_DEC_CASE(3)
+            SC_DEC_CASE(4)
+            SC_DEC_CASE(5)
+            SC_DEC_CASE(6)
 #undef SC_DEC_CASE
+        }
+        const int rc = check_launch("k_decompress");
+        if (rc) return rc;
+        start += count;
     }
-    return check_launch("k_decompress");
+    return SC_OK;
 }
 
 }  // extern "C"
