@@ -150,7 +150,7 @@ def bench_codec(args):
                      "traffic": None,
                      "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch"},
     }
-    return res, chunks, samples, cfg
+    return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
 
 
 def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
@@ -166,32 +166,51 @@ def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
     return int(len(idx))
 
 
-def cpu_baseline(model, chunks, samples_per_token, budget_s=20.0):
+def cpu_baseline(model, chunks, gpu_words, word_off, word_cnt, samples_per_token,
+                 n_compress=None, n_decode=512, decode_prefix=256):
     """CPU oracle (C restatement of the reference CPU backend) on a bounded
-    sample of the same chunks: compress then decompress, all host threads."""
+    sample of the same workload, all host threads:
+
+    * compress: 18 x threads random whole chunks (teacher-forced MLP batched
+      over each chunk, as CPUQuantMLPCompression.compress_chunks does);
+    * decompress: the first `decode_prefix` tokens of `n_decode` random
+      chunks decoded together, autoregressively, batched across chunks
+      (as CPUQuantMLPCompression.decompress_chunks batches up to 4,096);
+      the streams are the GPU's words, bit-identical to the oracle's.
+    Rates are converted to samples with the workload's samples per token;
+    the whole sample takes about 15 s on 16 host threads."""
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
     threads = oracle.cpu_count()
     oracle.set_num_threads(threads)
     om = oracle.OracleModel(model)
     rng = np.random.default_rng(1)
-    # calibrate with a few chunks, then size the sample to the budget
-    pick = list(rng.choice(len(chunks), size=min(len(chunks), 2 * threads), replace=False))
+    n_compress = n_compress or 18 * threads
+    pick = rng.choice(len(chunks), size=min(len(chunks), n_compress), replace=False)
     sample = [chunks[i] for i in pick]
     t0 = time.perf_counter()
-    comp = oracle.compress_chunks(om, sample)
+    oracle.compress_chunks(om, sample)
     tc = time.perf_counter() - t0
+    ctoks = sum(len(c) for c in sample)
+    dpick = rng.choice(len(chunks), size=min(len(chunks), n_decode), replace=False)
+    streams = [gpu_words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in dpick]
+    lens = [min(decode_prefix, len(chunks[i])) for i in dpick]
     t0 = time.perf_counter()
-    oracle.decompress_chunks(om, comp, [len(c) for c in sample])
+    dec = oracle.decompress_chunks(om, streams, lens)
     td = time.perf_counter() - t0
-    toks = sum(len(c) for c in sample)
-    sm = toks * samples_per_token
-    return {"value": round(sm / (tc + td) / 1e6, 5), "unit": "Msamples/s (round trip)",
-            "cores": threads, "kind": "port",
-            "compress_msamples_s": round(sm / tc / 1e6, 5),
-            "decompress_msamples_s": round(sm / td / 1e6, 5),
-            "sample": f"{len(sample)} random chunks ({toks} tokens) of the same workload, "
-                      f"compress + decompress with the C oracle on {threads} threads"}
+    for i, d in zip(dpick, dec):
+        if not np.array_equal(d, chunks[i][:len(d)]):
+            raise RuntimeError("CPU oracle decode disagrees with the GPU stream")
+    dtoks = sum(lens)
+    c_rate = ctoks * samples_per_token / tc
+    d_rate = dtoks * samples_per_token / td
+    return {"value": round(1.0 / (1.0 / c_rate + 1.0 / d_rate) / 1e6, 5),
+            "unit": "Msamples/s (round trip)", "cores": threads, "kind": "port",
+            "compress_msamples_s": round(c_rate / 1e6, 5),
+            "decompress_msamples_s": round(d_rate / 1e6, 5),
+            "sample": f"compress: {len(sample)} random whole chunks ({ctoks} tokens, {tc:.1f} s); "
+                      f"decompress: first {decode_prefix} tokens of {len(dpick)} random chunks decoded "
+                      f"together ({dtoks} tokens, {td:.1f} s); C oracle on {threads} threads"}
 
 
 def bench_mlp(args):
@@ -255,13 +274,13 @@ def main():
     if args.config == "c2":
         print(json.dumps(bench_mlp(args)), flush=True)
         return
-    res, chunks, samples, cfg = bench_codec(args)
+    res, chunks, samples, cfg, gpu_out = bench_codec(args)
     if not args.no_cpu_baseline:
         from sigcomp_amd.model_io import load_int_model, DEFAULT_QUANT_LOSSY_MODEL_PATH, DEFAULT_QUANT_LOSSLESS_MODEL_PATH
         model = load_int_model(DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy"
                                else DEFAULT_QUANT_LOSSLESS_MODEL_PATH)
         log("[bench] cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(model, chunks, samples / res["config"]["tokens"])
+        res["cpu_baseline"] = cpu_baseline(model, chunks, *gpu_out, samples / res["config"]["tokens"])
     print(json.dumps(res), flush=True)
 
 
