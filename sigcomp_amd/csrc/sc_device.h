@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace sc {
 
 constexpr int VOCAB = 256;
@@ -139,6 +141,16 @@ __device__ __forceinline__ uint32_t requant_u8_fast(int acc, int bias, int m0, u
     const int biased = (int)((uint32_t)acc + (uint32_t)bias);
     const int s = __mulhi(biased, m0) >> shift32;
     return (uint32_t)(uint8_t)(int8_t)min(max(s, lo), 127);
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1, so
+// that arrays indexed by I stay in registers however large the body is.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
 }
 
 // ---------------------------------------------------------------- MFMA GEMMs
@@ -435,27 +447,27 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
     }
     uint32_t *par = s_par + wave * 4 * PAR_DWORDS;
     uint32_t pk[PASSES][NTP][RT][4];
-#pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) {
+    static_for<PASSES>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int pass = decltype(pc)::value;
         const int nt0 = ntw0 + pass * NTP;
         v16i acc[NTP][RT];
         zero_acc(acc);
         const WStream ws = make_wstream(L.w, L.bytes);
         if constexpr (FIRST) gemm_layer0<NTP, RT>(ws, nt0, s_emb, tok, acc, lane);
         else gemm_hidden<NTP, RT, KTH>(ws, nt0, s_act, acc, lane);
-        if (pass == 0) {
+        if constexpr (pass == 0) {
 #pragma unroll
             for (int d = 0; d < PL; ++d)
                 if (d * 64 + lane < PW) par[d * 64 + lane] = pr[d];
         }
         requant_pack(acc, L, par + pass * NTP * PAR_DWORDS, lane, pk[pass]);
-    }
+    });
     if constexpr (!FIRST) __syncthreads();
-#pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) {
+    static_for<PASSES>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int pass = decltype(pc)::value;
         if constexpr (LAST) store_packed(pk[pass], ntw0 + pass * NTP, s_act, lane);
         else store_packed_perm(pk[pass], ntw0 + pass * NTP, s_act, lane);
-    }
+    });
     __syncthreads();
 }
 
