@@ -83,6 +83,14 @@ int sc_model_destroy(sc_model *model);
 /* Device copy of the model's exp LUT (uint64 [256]); owned by the model. */
 const uint64_t *sc_model_lut(const sc_model *model);
 
+/* MLP core the model runs on: 1 = pipelined core (every layer's requant
+ * constants satisfy m0 < 2**31 and shift >= 32 after the m0 = 2**31
+ * rewrite, ReLU on every layer but the last; tiles of up to 128 rows), 0 =
+ * plain core (any valid model; also selected by SC_HIP_PLAIN_CORE=1 in the
+ * environment at sc_model_create).  Both give identical results.  No
+ * reference counterpart (diagnostic). */
+int sc_model_core(const sc_model *model);
+
 /* MLP forward on explicit context windows: ctx int64 [rows, 64] (device,
  * tokens in [0, 256]) -> logits int8 [rows, 256] (device).  Replaces
  * GPUBitExactMLPDecoder._ar_step (quant_mlp_export.py:133-138) = int8

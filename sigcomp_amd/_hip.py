@@ -23,6 +23,7 @@ SC_STATUS_BAD_TOKEN = 3
 
 EXPORTED = (
     "sc_last_error", "sc_version", "sc_model_create", "sc_model_destroy", "sc_model_lut",
+    "sc_model_core",
     "sc_mlp_forward", "sc_mlp_forward_cdf", "sc_logits_to_cdf", "sc_encode_step",
     "sc_encode_seal", "sc_decode_step", "sc_compress_workspace_bytes", "sc_compress_chunks",
     "sc_decompress_chunks",
@@ -73,6 +74,7 @@ def lib():
         L.sc_model_destroy.argtypes = [_P]
         L.sc_model_lut.argtypes = [_P]
         L.sc_model_lut.restype = _P
+        L.sc_model_core.argtypes = [_P]
         L.sc_mlp_forward.argtypes = [_P, _P, _I64, _P, _P, _P]
         L.sc_mlp_forward_cdf.argtypes = [_P, _P, _I64, _P, _P, _P]
         L.sc_logits_to_cdf.argtypes = [_P, _I64, _P, _P, _P]

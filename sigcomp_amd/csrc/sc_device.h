@@ -58,7 +58,7 @@ struct ModelDev {
     const int8_t *emb;       // [257][128] row-major
     const uint64_t *lut;     // [256]
     int32_t n_layers;
-    int32_t pad;
+    int32_t pipe;            // every layer fast, ReLU on all but the last: pipelined core usable
 };
 
 // ---------------------------------------------------------------- LDS layouts
@@ -264,14 +264,17 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
 // so a position is PD = 4 k-steps.  Same pipeline as gemm_hidden over pairs
 // of positions; tokens are read two positions ahead and turned into table
 // addresses one position ahead.
-template <int NTP, int RT, class TokFn>
-__device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
-                                            TokFn tok, v16i (&acc)[NTP][RT], int lane) {
+//
+// General form: n-tile of accumulator j is nt(j), accumulator tile (j, i) is
+// acc(j, i) (a reference); the form below it covers n-tiles nt0 .. nt0+NTP-1.
+template <int NTP, int RT, class TokFn, class NtFn, class AccFn>
+__device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, const uint8_t *s_emb, TokFn tok,
+                                                AccFn acc, int lane) {
     constexpr int PD = 4;
     static_assert(WIN % 2 == 0, "positions are processed in pairs");
     int voff[NTP];
 #pragma unroll
-    for (int j = 0; j < NTP; ++j) voff[j] = (nt0 + j) * KT0 * 1024 + lane * 16;
+    for (int j = 0; j < NTP; ++j) voff[j] = nt(j) * KT0 * 1024 + lane * 16;
     v4i w[2][PD][NTP];
 #pragma unroll
     for (int s = 0; s < PD; ++s)
@@ -319,14 +322,23 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
 #pragma unroll
                 for (int j = 0; j < NTP; ++j)
 #pragma unroll
-                    for (int i = 0; i < RT; ++i)
-                        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i], acc[j][i],
-                                                                          0, 0, 0);
+                    for (int i = 0; i < RT; ++i) {
+                        v16i &a = acc(j, i);
+                        a = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i], a, 0, 0, 0);
+                    }
                 kstep_schedule<NTP, RT>();
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
+}
+
+template <int NTP, int RT, class TokFn>
+__device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
+                                            TokFn tok, v16i (&acc)[NTP][RT], int lane) {
+    gemm_layer0_map<NTP, RT>(
+        ws, [&](int j) { return nt0 + j; }, s_emb, tok,
+        [&](int j, int i) -> v16i & { return acc[j][i]; }, lane);
 }
 
 // Requantise accumulators to packed int8.  Accumulator element v of tile

@@ -3,12 +3,14 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
 
 #include "../../include/sigcomp_hip.h"
 #include "sc_device.h"
+#include "sc_pipe.h"
 
 using namespace sc;
 
@@ -29,15 +31,30 @@ constexpr int DEC_RT_MAX = 6;       // decode: up to 192 chunks per workgroup
 
 enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
 
-template <int MODE>
+// MLP core of one tile: the pipelined core when the model allows it.
+template <bool PIPE, int RT, class TokFn>
+__device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act, uint32_t *s_par,
+                                         TokFn tok, int wave, int lane) {
+    if constexpr (PIPE) mlp_rows_pipe<RT>(M, s_emb, s_act, s_par, tok, wave, lane);
+    else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, tok, wave, lane);
+}
+template <bool PIPE>
+constexpr int par_lds_dwords() { return PIPE ? PIPE_PAR_DWORDS : PAR_LDS_DWORDS; }
+// activation row layout of the core: padded rows (pipelined) or swizzled rows
+template <bool PIPE>
+constexpr int act_row_bytes() { return PIPE ? PACT_ROW : ACT_ROW; }
+template <bool PIPE>
+__device__ __forceinline__ int act_at(int r, int chunk) { return PIPE ? pact_off(r, chunk) : act_off(r, chunk); }
+
+template <int MODE, bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const int64_t *__restrict__ ctx,
                                                             int64_t rows, int8_t *__restrict__ logits,
                                                             int32_t *__restrict__ cdf,
                                                             int32_t *__restrict__ status) {
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
@@ -59,20 +76,20 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
-        mlp_rows<RT_TILE, 1>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
-                             wave, lane);
+        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+                                wave, lane);
         if (MODE == OUT_LOGITS) {
             // 128 rows x 256 bytes, 16-byte chunks, coalesced
             for (int i = threadIdx.x; i < R_TILE * 16; i += THREADS) {
                 const int r = i >> 4, c = i & 15;
                 if (row0 + r < rows)
-                    *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_off(r, c));
+                    *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_at<PIPE>(r, c));
             }
         } else {
             for (int gi = wave; gi < R_TILE / 4; gi += WAVES) {
                 const int r = gi * 4 + q4;
                 Freq16 fr;
-                row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
+                row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
                 if (row0 + r < rows) {
                     int32_t *dst = cdf + (row0 + r) * (VOCAB + 1) + 16 * u;
                     uint32_t c = fr.ex;
@@ -93,14 +110,15 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
 // Workgroups take whole chunks from a work counter; tiles of 128 consecutive
 // steps of one chunk share a 192-token window in LDS.  Output per token:
 // (exclusive cumulative frequency, frequency) of the token actually coded.
+template <bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
                                                              const int64_t *__restrict__ tok_off,
                                                              const int32_t *__restrict__ lengths,
                                                              int64_t n_chunks, uint2 *__restrict__ pairs,
                                                              unsigned int *__restrict__ counter) {
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * ACT_ROW];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ double s_lut[VOCAB];
     __shared__ int64_t s_unit;
@@ -124,13 +142,13 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                 s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
             }
             __syncthreads();
-            mlp_rows<RT_TILE, 1>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
-                                 wave, lane);
+            mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
+                                    wave, lane);
             const int32_t valid = min(R_TILE, L - t0);
             for (int gi = wave; gi * 4 < valid; gi += WAVES) {
                 const int r = gi * 4 + q4;
                 Freq16 fr;
-                row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
+                row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
                 const int s = s_tok[r + WIN];
                 if (r < valid && (s >> 4) == u) {
                     uint32_t cum, freq;
@@ -183,7 +201,7 @@ __global__ void k_zero_u32(unsigned int *p, int n) {
 // windows (kept as 64-token rings in LDS), the fused frequency step and one
 // decoder step per chunk; the decoded token is appended to the ring.  Chunks
 // are independent, so workgroups never synchronise with each other.
-template <int RT>
+template <int RT, bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
                                                            const int64_t *__restrict__ word_off,
                                                            const int32_t *__restrict__ word_cnt,
@@ -193,9 +211,9 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                                            int32_t *__restrict__ status) {
     constexpr int R = 32 * RT;
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t s_act[R * ACT_ROW];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[PAR_LDS_DWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
     __shared__ int64_t s_woff[R], s_toff[R];
@@ -237,15 +255,15 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __syncthreads();
     const int32_t maxlen = s_maxlen;
     for (int32_t t = 0; t < maxlen; ++t) {
-        mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par,
-                     [&](int r, int p) {
-                         return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
-                     },
-                     wave, lane);
+        mlp_tile<PIPE, RT>(M, s_emb, s_act, s_par,
+                           [&](int r, int p) {
+                               return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
+                           },
+                           wave, lane);
         for (int gi = wave; gi < R / 4; gi += WAVES) {
             const int r = gi * 4 + q4;
             Freq16 fr;
-            row_frequencies16(row_logits16(s_act, r, u), s_lut, u, fr);
+            row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
             // _decode_partition (cpu_entropy_coding.py:230-266); the 16 lanes
             // of the row compute the same state, lane u == 0 stores it
             const bool active = t < s_len[r] && s_stat[r] == 0;
@@ -515,6 +533,15 @@ std::vector<int8_t> pack_weight(const int8_t *w, int n, int k, bool perm_k) {
 
 hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
+template <int RT>
+void dec_launch(const sc_model *m, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
+                const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
+                int32_t *st) {
+    auto *kern = m->dev.pipe && RT <= 4 ? k_decompress<RT, (RT <= 4)> : k_decompress<RT, false>;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, s, m->dev, words, woff, wcnt, len, count, tokens, toff,
+                       st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -618,6 +645,11 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         D.bytes = (int32_t)packed.size();
     }
     m->dev.n_layers = n_layers;
+    // SC_HIP_PLAIN_CORE=1 at model creation selects the plain core (testing)
+    const char *plain = getenv("SC_HIP_PLAIN_CORE");
+    m->dev.pipe = plain && plain[0] == '1' ? 0 : 1;
+    for (int i = 0; i < n_layers; ++i)
+        if (!m->dev.layer[i].fast || m->dev.layer[i].relu != (i < n_layers - 1 ? 1 : 0)) m->dev.pipe = 0;
     if (rc != SC_OK) {
         sc_model_destroy(m);
         return rc;
@@ -636,6 +668,8 @@ int sc_model_destroy(sc_model *m) {
 
 const uint64_t *sc_model_lut(const sc_model *m) { return m ? m->dev.lut : nullptr; }
 
+int sc_model_core(const sc_model *m) { return m && m->dev.pipe ? 1 : 0; }
+
 static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t rows, int8_t *logits,
                               int32_t *cdf, int32_t *status, void *stream, int mode) {
     if (!m || rows < 0 || !status) return fail(SC_ERR_ARG, "bad argument");
@@ -645,12 +679,10 @@ static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t row
     DeviceGuard guard(m->device);
     const int64_t tiles = (rows + R_TILE - 1) / R_TILE;
     const int grid = (int)std::min<int64_t>(tiles, m->n_cu);
-    if (mode == OUT_LOGITS)
-        hipLaunchKernelGGL(k_mlp_context<OUT_LOGITS>, dim3(grid), dim3(THREADS), 0, as_stream(stream),
-                           m->dev, ctx, rows, logits, cdf, status);
-    else
-        hipLaunchKernelGGL(k_mlp_context<OUT_CDF32>, dim3(grid), dim3(THREADS), 0, as_stream(stream),
-                           m->dev, ctx, rows, logits, cdf, status);
+    auto *kern = mode == OUT_LOGITS ? (m->dev.pipe ? k_mlp_context<OUT_LOGITS, true> : k_mlp_context<OUT_LOGITS, false>)
+                                    : (m->dev.pipe ? k_mlp_context<OUT_CDF32, true> : k_mlp_context<OUT_CDF32, false>);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, as_stream(stream), m->dev, ctx, rows, logits, cdf,
+                       status);
     return check_launch("k_mlp_context");
 }
 
@@ -737,7 +769,8 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
     int rc = check_launch("k_zero_u32");
     if (rc) return rc;
     const int grid = (int)std::min<int64_t>(n_chunks, m->n_cu);
-    hipLaunchKernelGGL(k_compress_mlp, dim3(grid), dim3(THREADS), 0, s, m->dev, tokens, tok_off, lengths, n_chunks,
+    hipLaunchKernelGGL(m->dev.pipe ? k_compress_mlp<true> : k_compress_mlp<false>, dim3(grid), dim3(THREADS), 0, s,
+                       m->dev, tokens, tok_off, lengths, n_chunks,
                        pairs, counter);
     rc = check_launch("k_compress_mlp");
     if (rc) return rc;
@@ -783,8 +816,7 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
         switch (rt) {
 #define SC_DEC_CASE(N)                                                                                        \
     case N:                                                                                                   \
-        hipLaunchKernelGGL(k_decompress<N>, dim3(grid), dim3(THREADS), 0, s, m->dev, wds, woff, wcnt, len,     \
-                           count, tokens, toff, st);                                                          \
+        dec_launch<N>(m, grid, s, wds, woff, wcnt, len, count, tokens, toff, st);                             \
         break;
             SC_DEC_CASE(1)
             SC_DEC_CASE(2)

@@ -1,0 +1,297 @@
+// sc_pipe.h -- software-pipelined MLP core for tiles of up to 128 rows.
+//
+// The plain core (mlp_rows) requantises a layer after its GEMM, with the
+// matrix cores idle.  Here every layer runs as two passes of two n-tiles per
+// wave and the requantisation of one pass is interleaved, instruction by
+// instruction, with the MFMA stream of the next GEMM segment:
+//
+//   pass p of wave w computes n-tiles 8p + 2w, 8p + 2w + 1, so pass 0 of all
+//   waves yields features 0..255 (region A of an activation row, the next
+//   layer's k-tiles 0..7) and pass 1 features 256..511 (region B, k-tiles
+//   8..15).  Per hidden layer l (steps v = 0..31: pass 0 k 0..15, pass 1 k 0..15):
+//
+//     v  0.. 7  pass 0, k-tiles 0..7 (region A)   || requant of layer l-1 pass 1
+//               store layer l-1 pass 1 -> region B; barrier
+//     v  8..15  pass 0, k-tiles 8..15 (region B)
+//     v 16..31  pass 1, all k-tiles                || requant of layer l pass 0
+//               barrier; store layer l pass 0 -> region A; barrier
+//
+//   A region is overwritten only after a barrier that ends every read of it.
+//   Weight fragments are prefetched PPD k-steps ahead across pass and layer
+//   boundaries.  Accumulators of the two passes take 2 x 2 x RT x 16 AGPRs
+//   (256 for RT = 4).
+//
+// Requires every layer to take the 32-bit requant path (LayerDev::fast), ReLU
+// on all layers but the last, and 512-wide hidden layers (ModelDev::pipe).
+#pragma once
+
+#include "sc_device.h"
+
+namespace sc {
+
+constexpr int PNT = 2;                               // n-tiles per pass
+constexpr int PPD = 4;                               // weight prefetch distance (k-steps)
+constexpr int PBLK = PNT * PAR_DWORDS;               // parameter dwords of one pass
+constexpr int PBLK_LANE = (PBLK + 63) / 64;
+// LDS parameter slots per wave: 0 = pass 0 of the current layer, 1 and 2 =
+// pass 1 of even / odd layers (read while the next layer runs).
+constexpr int PIPE_PAR_DWORDS = WAVES * 3 * PBLK;
+
+// Requant parameters of packed group g of n-tile j (lane half g2).
+struct RqPar {
+    v4i bb, mm;
+    uint32_t sh;
+};
+
+__device__ __forceinline__ RqPar rq_par(const uint32_t *blk, int j, int g, int g2) {
+    const uint32_t *pj = blk + j * PAR_DWORDS;
+    const int o = 8 * g + 4 * g2;
+    RqPar p;
+    p.bb = *(const v4i *)(pj + o);
+    p.mm = *(const v4i *)(pj + 32 + o);
+    p.sh = pj[64 + (o >> 2)];
+    return p;
+}
+
+// Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile -> packed int8.
+template <bool RELU>
+__device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar &p) {
+    constexpr int lo = RELU ? 0 : -128;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t q = requant_u8_fast(acc[4 * g + e], p.bb[e], p.mm[e], (p.sh >> (8 * e)) & 63u, lo);
+        packed |= q << (8 * e);
+    }
+    return packed;
+}
+
+__device__ __forceinline__ v4i wload_s(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    v4u x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    return (v4i)x;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t layer_rsrc(const LayerDev &L) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)L.w, (short)0, L.bytes, 0x00020000);
+}
+
+// Parameter blocks of one pass (n-tiles nt0, nt0 + 1) into registers / LDS.
+__device__ __forceinline__ void par_fetch(const uint32_t *gpar, int nt0, int lane, uint32_t (&pr)[PBLK_LANE]) {
+#pragma unroll
+    for (int d = 0; d < PBLK_LANE; ++d) {
+        const int idx = d * 64 + lane;
+        pr[d] = idx < PBLK ? gpar[nt0 * PAR_DWORDS + idx] : 0u;
+    }
+}
+__device__ __forceinline__ void par_put(uint32_t *blk, const uint32_t (&pr)[PBLK_LANE], int lane) {
+#pragma unroll
+    for (int d = 0; d < PBLK_LANE; ++d)
+        if (d * 64 + lane < PBLK) blk[d * 64 + lane] = pr[d];
+}
+
+// Activation rows of the pipelined core are padded to PACT_ROW bytes instead
+// of swizzled: 16 consecutive rows reading the same 16-byte chunk start 16
+// bytes apart modulo the 256-byte bank window, so they hit 16 different bank
+// groups, and chunk c of a row sits at a constant offset c*16 from the row
+// base (an immediate of the LDS instruction).
+constexpr int PACT_ROW = ACT_ROW + 16;
+__device__ __forceinline__ int pact_off(int r, int chunk) { return r * PACT_ROW + chunk * 16; }
+
+// B fragments of hidden k-tile kt for the RT row tiles; `base` = pact_off(rl, g).
+template <int RT>
+__device__ __forceinline__ void read_b(const uint8_t *s_act, int base, int kt, v4i (&b)[RT]) {
+#pragma unroll
+    for (int i = 0; i < RT; ++i) b[i] = *(const v4i *)(s_act + base + i * 32 * PACT_ROW + kt * 32);
+}
+
+// Packed results in the padded layout: hidden order (as store_packed_perm)
+// and natural order (as store_packed).
+template <int RT>
+__device__ __forceinline__ void pstore_perm(const uint32_t (&pk)[PNT][RT][4], int nt0, uint8_t *s_act, int lane) {
+    const int rl = lane & 31, g2 = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < PNT; ++j)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            const v4i v = {(int)pk[j][i][0], (int)pk[j][i][1], (int)pk[j][i][2], (int)pk[j][i][3]};
+            *(v4i *)(s_act + pact_off(i * 32 + rl, (nt0 + j) * 2 + g2)) = v;
+        }
+}
+template <int RT>
+__device__ __forceinline__ void pstore_natural(const uint32_t (&pk)[PNT][RT][4], int nt0, uint8_t *s_act, int lane) {
+    const int rl = lane & 31, g2 = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < PNT; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+                *(uint32_t *)(s_act + pact_off(i * 32 + rl, 0) + (nt0 + j) * 32 + 8 * g + 4 * g2) = pk[j][i][g];
+}
+
+// Instruction order of one pipelined k-step: the step's LDS reads and weight
+// loads are spread over its first MFMAs, and VA VALU instructions (the
+// interleaved requantisation) follow every MFMA.
+template <int MF, int DS, int VM, int VA>
+__device__ __forceinline__ void pipe_schedule() {
+    static_for<MF>([&](auto mc) __attribute__((always_inline)) {
+        constexpr int m = decltype(mc)::value;
+        if constexpr (m < DS) __builtin_amdgcn_sched_group_barrier(0x100, DS > MF && m == MF - 1 ? DS - m : 1, 0);
+        if constexpr (m < VM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (VA > 0) __builtin_amdgcn_sched_group_barrier(0x002, VA, 0);
+    });
+}
+
+// One hidden layer (LASTL = false) or the output layer (LASTL = true, one
+// pass: n-tiles 2w, 2w+1 = logits 64w .. 64w+63, stored in natural order).
+// Entry: accB = layer l-1 pass 1 (not yet requantised, parameters in slot
+// `prev_slot`), region A = layer l-1 pass 0 (visible to all waves),
+// w[0][*] = this layer's first PPD weight k-steps.  Exit: accB = this
+// layer's pass 1, slot `cur_slot` = its parameters, region A = this layer's
+// pass 0 (visible), w[0][*] = the next layer's first k-steps.
+template <int RT, bool LASTL>
+__device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
+                                            uint32_t *s_parw, int prev_slot, int cur_slot,
+                                            v16i (&accA)[PNT][RT], v16i (&accB)[PNT][RT],
+                                            v4i (&w)[2][PPD][PNT], uint32_t (&pk)[PNT][RT][4], int wave,
+                                            int lane) {
+    constexpr int NV = LASTL ? KTH : 2 * KTH;
+    constexpr int MF = PNT * RT;
+    constexpr int RH = (RT + 1) / 2;          // row tiles requantised in the first of two steps
+    const int g = lane >> 5, voff = lane * 16;
+    const int bbase = pact_off(lane & 31, g);
+    const __amdgpu_buffer_rsrc_t rs = layer_rsrc(L);
+    const __amdgpu_buffer_rsrc_t rsn = layer_rsrc(Ln);
+    const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;   // n-tile bases of pass 0 / pass 1
+    const uint32_t *prev = s_parw + prev_slot * PBLK;
+    uint32_t *blk0 = s_parw;
+    uint32_t *blkc = s_parw + cur_slot * PBLK;
+    uint32_t pr0[PBLK_LANE], pr1[PBLK_LANE];
+    par_fetch(L.par, nb0, lane, pr0);
+    if constexpr (!LASTL) par_fetch(L.par, nb1, lane, pr1);
+    v4i b[2][RT];
+    read_b<RT>(s_act, bbase, 0, b[0]);
+    RqPar pp = rq_par(prev, 0, 0, g);
+    const v16i zero = {};
+    static_for<NV>([&](auto vc) __attribute__((always_inline)) {
+        constexpr int v = decltype(vc)::value;
+        constexpr int pass = v / KTH, kt = v % KTH, set = (v / PPD) & 1, slot = v % PPD;
+        // next step's B fragments (none across a barrier)
+        if constexpr (v != 7 && v != NV - 1) read_b<RT>(s_act, bbase, (kt + 1) % KTH, b[(kt + 1) & 1]);
+        // weights PPD steps ahead: this layer, else the next layer's pass 0
+        constexpr int vp = v + PPD;
+        if constexpr (vp < NV) {
+            constexpr int pp_ = vp / KTH, kp = vp % KTH;
+#pragma unroll
+            for (int j = 0; j < PNT; ++j)
+                w[(vp / PPD) & 1][vp % PPD][j] = wload_s(rs, voff, (((pp_ ? nb1 : nb0) + j) * KTH + kp) * 1024);
+        } else if constexpr (!LASTL) {
+            constexpr int kn = vp - NV;
+#pragma unroll
+            for (int j = 0; j < PNT; ++j)
+                w[(vp / PPD) & 1][vp % PPD][j] = wload_s(rsn, voff, ((nb0 + j) * KTH + kn) * 1024);
+        }
+        // side work: parameters one step ahead, then requantised words
+        constexpr int VA = v < 8 ? 12 : (!LASTL && v >= 16 ? 6 : 0);
+        if constexpr (v < 8) {
+            constexpr int j = v / 4, gg = v % 4;
+            const RqPar cur = pp;
+            if constexpr (v + 1 < 8) pp = rq_par(prev, (v + 1) / 4, (v + 1) % 4, g);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
+        } else if constexpr (!LASTL && v >= 16) {
+            constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
+            const RqPar cur = pp;
+            if constexpr (u + 1 < 16) pp = rq_par(blk0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
+#pragma unroll
+            for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
+        }
+        // this step's MFMAs
+        auto &acc = pass == 0 ? accA : accB;
+#pragma unroll
+        for (int j = 0; j < PNT; ++j)
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[set][slot][j], b[kt & 1][i],
+                                                                  kt == 0 ? zero : acc[j][i], 0, 0, 0);
+        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 3, PNT, VA>();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (v == 7) {
+            // layer l-1 pass 1 -> region B; this layer's parameters -> LDS
+            pstore_perm<RT>(pk, nb1, s_act, lane);
+            par_put(blk0, pr0, lane);
+            if constexpr (!LASTL) {
+                par_put(blkc, pr1, lane);
+                pp = rq_par(blk0, 0, 0, g);   // first parameters of the pass-0 requantisation
+            }
+            __syncthreads();
+            read_b<RT>(s_act, bbase, 8, b[0]);
+        }
+    });
+    if constexpr (LASTL) {
+        requant_pack_t<PNT, RT, true, false>(accA, blk0, lane, pk);
+        __syncthreads();
+        pstore_natural<RT>(pk, nb0, s_act, lane);
+    } else {
+        __syncthreads();
+        pstore_perm<RT>(pk, nb0, s_act, lane);
+    }
+    __syncthreads();
+}
+
+// One MLP evaluation of R = 32*RT rows (RT <= 4), same contract as mlp_rows
+// but in the padded row layout: entered after a barrier that ends every read
+// of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of
+// each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS.
+template <int RT, class TokFn>
+__device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
+                                              uint32_t *s_par, TokFn tok, int wave, int lane) {
+    static_assert(RT >= 1 && RT <= 4, "two passes of accumulators must fit the AGPRs");
+    static_assert(WAVES * 2 * PNT * 32 == HID && WAVES * PNT * 32 == VOCAB, "tile split assumes 4 waves");
+    // wave-uniform in a scalar register: weight offsets go to the scalar
+    // offset of the buffer loads
+    wave = __builtin_amdgcn_readfirstlane(wave);
+    const int voff = lane * 16;
+    const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;
+    uint32_t *s_parw = s_par + wave * 3 * PBLK;
+    v16i accA[PNT][RT], accB[PNT][RT];
+    v4i w[2][PPD][PNT];
+    uint32_t pk[PNT][RT][4];
+    // layer 0 in one pass over both passes' n-tiles (each embedding B
+    // fragment is read from LDS once), then the pass-0 requantisation and
+    // store (no wave reads s_act during layer 0); pass 1 stays in accB for
+    // the first hidden layer; then that layer's first weights
+    {
+        const LayerDev &L0 = M.layer[0];
+        uint32_t pr0[PBLK_LANE], pr1[PBLK_LANE];
+        par_fetch(L0.par, nb0, lane, pr0);
+        par_fetch(L0.par, nb1, lane, pr1);
+        const WStream ws = make_wstream(L0.w, L0.bytes);
+        zero_acc(accA);
+        zero_acc(accB);
+        gemm_layer0_map<2 * PNT, RT>(
+            ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, tok,
+            [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; }, lane);
+        par_put(s_parw, pr0, lane);
+        par_put(s_parw + 1 * PBLK, pr1, lane);
+        requant_pack_t<PNT, RT, true, true>(accA, s_parw, lane, pk);
+        pstore_perm<RT>(pk, nb0, s_act, lane);
+        const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
+#pragma unroll
+        for (int s = 0; s < PPD; ++s)
+#pragma unroll
+            for (int j = 0; j < PNT; ++j) w[0][s][j] = wload_s(rs1, voff, ((nb0 + j) * KTH + s) * 1024);
+        __syncthreads();
+    }
+    const int last = M.n_layers - 1;
+#pragma unroll 1
+    for (int l = 1; l < last; ++l)
+        pipe_hidden<RT, false>(M.layer[l], M.layer[l + 1], s_act, s_parw, 1 + ((l - 1) & 1), 1 + (l & 1), accA,
+                               accB, w, pk, wave, lane);
+    pipe_hidden<RT, true>(M.layer[last], M.layer[last], s_act, s_parw, 1 + ((last - 1) & 1), 0, accA, accB, w, pk,
+                          wave, lane);
+}
+
+}  // namespace sc

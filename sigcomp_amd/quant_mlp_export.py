@@ -60,6 +60,8 @@ class HipModel:
                                                   ctypes.byref(handle)))
         self.handle = handle
         self.exp_lut = torch.from_numpy(lut.copy()).to(self.device)
+        # True when the kernels run the pipelined MLP core (see sc_model_core)
+        self.pipelined = bool(_hip.lib().sc_model_core(handle))
 
     def __del__(self):
         h = getattr(self, "handle", None)

@@ -180,3 +180,56 @@ def test_empty_inputs(codecs):
     assert codecs["lossless"].batch_inference_reads(list_of_reads=[np.zeros(0, np.uint8)]) == [b""]
     out = codecs["lossless"].batch_inference_reads(list_of_compressed_reads=[b""], list_of_lengths=[0])
     assert len(out) == 1 and out[0].size == 0
+
+
+def _plain_and_generic_models():
+    """Models that run the plain (non-pipelined) MLP core: the bundled lossless
+    model with the core forced by SC_HIP_PLAIN_CORE, and a random model whose
+    layer 3 needs the 64-bit requantisation (shift < 32 with m0 = 2**31, and
+    m0 = 2**31 - 1), which the pipelined core does not take."""
+    import dataclasses
+    from sigcomp_amd.model_io import load_int_model, make_layer, random_int_model
+    lossless = load_int_model()
+    m = random_int_model(seed=21, per_channel=True)
+    L = m.layers[3]
+    n = L.n
+    m0 = np.where(np.arange(n) % 2 == 0, 1 << 31, (1 << 31) - 1).astype(np.int64)
+    shift = np.full(n, 41, np.int32)
+    shift[::7] = 31
+    w = (L.weight // 16).astype(np.int8)
+    layers = list(m.layers)
+    layers[3] = make_layer(w, L.bias // 64, m0, shift, True)
+    return lossless, dataclasses.replace(m, layers=layers)
+
+
+@pytest.mark.parametrize("which", ["plain_lossless", "generic_requant"])
+def test_plain_core_matches_oracle(oracle_mod, monkeypatch, which):
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    lossless, generic = _plain_and_generic_models()
+    if which == "plain_lossless":
+        monkeypatch.setenv("SC_HIP_PLAIN_CORE", "1")
+        model = lossless
+    else:
+        model = generic
+    codec = QuantMLPCompression(chunk_len=2048, gpu=0, model=model)
+    monkeypatch.delenv("SC_HIP_PLAIN_CORE", raising=False)
+    assert not codec.hip.pipelined
+    om = oracle_mod.OracleModel(model)
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(0, 257, (300, 64))
+    ctx[:50, :30] = 256
+    exp = oracle_mod.mlp_forward(om, ctx)
+    got = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
+    assert np.array_equal(got, exp)
+    cdf = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "cdf").cpu().numpy()
+    assert np.array_equal(cdf.astype(np.int64), oracle_mod.logits_to_cdf(exp, model.exp_lut))
+    lengths = [1, 64, 65, 300, 129]
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    gpu = codec.compress_chunks(chunks)
+    assert gpu == oracle_mod.compress_chunks(om, chunks)
+    back = codec.decompress_chunks(gpu, lengths)
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+
+
+def test_pipelined_core_selected_for_bundled_models(codecs):
+    assert codecs["lossless"].hip.pipelined and codecs["lossy"].hip.pipelined
