@@ -96,6 +96,15 @@ def bench_codec(args):
                                           _hip.ptr(o_len), n, _hip.ptr(out_tokens), _hip.ptr(o_toff),
                                           _hip.ptr(dstatus), stream.cuda_stream))
 
+    if args.copy_mib:
+        # one plain elementwise kernel moving a known number of bytes (read
+        # copy_mib MiB, write copy_mib MiB), outside the timed region: the
+        # reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     with torch.cuda.device(dev), torch.cuda.stream(stream):
         for w in range(args.warmup):
             compress(); decompress()
@@ -266,6 +275,8 @@ def main():
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="run one elementwise copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the codec shards by independent reads with no "

@@ -156,7 +156,8 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
                    int64_t B, const sc_decoder_state *state, const uint32_t *words,
                    int64_t *symbols_out, void *stream);
 
-/* Bytes of device workspace sc_compress_chunks needs for n_tokens tokens. */
+/* Bytes of device workspace sc_compress_chunks needs for n_tokens tokens in
+ * n_chunks chunks (a tile table, 4 bytes per chunk, and 8 bytes per token). */
 int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks);
 
 /* Compress n_chunks independent token chunks (teacher-forced MLP over every
@@ -179,8 +180,9 @@ int sc_compress_chunks(const sc_model *model, const uint8_t *tokens, const int64
  * fused frequency step and decoder step per token, context kept on chip).
  * Chunk c: word_cnt[c] words at words + word_off[c] -> lengths[c] tokens at
  * tokens + tok_off[c]; status[c] is written (SC_STATUS_INVALID_STREAM on a
- * corrupt stream).  All arrays device.  Chunks sorted by descending length
- * (as QuantMLPCompression passes them) give the shortest schedule: the
+ * corrupt stream, whose tokens are then unspecified).  All arrays device.
+ * Chunks sorted by descending length (as QuantMLPCompression passes them)
+ * give the shortest schedule: the
  * shortest chunks then land in the final, partial launch.  Replaces
  * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
  * (quant_mlp_export.py:325-377); output equals

@@ -107,56 +107,96 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
 
 // ---- compress: teacher-forced MLP fused with the frequency step ----------
 
-// Workgroups take whole chunks from a work counter; tiles of 128 consecutive
-// steps of one chunk share a 192-token window in LDS.  Output per token:
-// (exclusive cumulative frequency, frequency) of the token actually coded.
+// Tiles are 128 consecutive steps of one chunk.  tile_start[c] = number of
+// tiles of chunks 0 .. c-1 (exclusive scan of ceil(lengths[c] / 128)),
+// tile_start[n_chunks] = total.  One workgroup of 1024 threads: every thread
+// scans a contiguous segment, segment sums are scanned in LDS.
+constexpr int SCAN_THREADS = 1024;
+
+__global__ __launch_bounds__(SCAN_THREADS) void k_tile_scan(const int32_t *__restrict__ lengths, int64_t n_chunks,
+                                                             int32_t *__restrict__ tile_start) {
+    __shared__ int32_t s_sum[SCAN_THREADS];
+    const int64_t per = (n_chunks + SCAN_THREADS - 1) / SCAN_THREADS;
+    const int64_t c0 = threadIdx.x * per, c1 = min(c0 + per, n_chunks);
+    int32_t sum = 0;
+    for (int64_t c = c0; c < c1; ++c) sum += (lengths[c] + R_TILE - 1) / R_TILE;
+    s_sum[threadIdx.x] = sum;
+    __syncthreads();
+    for (int d = 1; d < SCAN_THREADS; d <<= 1) {
+        const int32_t v = threadIdx.x >= (unsigned)d ? s_sum[threadIdx.x - d] : 0;
+        __syncthreads();
+        s_sum[threadIdx.x] += v;
+        __syncthreads();
+    }
+    int32_t run = s_sum[threadIdx.x] - sum;
+    for (int64_t c = c0; c < c1; ++c) {
+        tile_start[c] = run;
+        run += (lengths[c] + R_TILE - 1) / R_TILE;
+    }
+    if (threadIdx.x == SCAN_THREADS - 1) tile_start[n_chunks] = s_sum[SCAN_THREADS - 1];
+}
+
+// Workgroup b runs tiles b, b + G, b + 2G, ... (G = grid size) of the global
+// tile order.  Every tile costs the same, so the workgroups stay in step and
+// stream the same layer's weights at the same time: each XCD's L2 then
+// serves one weight fragment to all of its CUs (a work counter lets
+// workgroups drift apart, and the L2 cycles through the whole model).  A
+// tile's 128 + 64 tokens (64 of left context) are staged in LDS.  Output per
+// token: (exclusive cumulative frequency, frequency) of the coded token.
 template <bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
                                                              const int64_t *__restrict__ tok_off,
                                                              const int32_t *__restrict__ lengths,
-                                                             int64_t n_chunks, uint2 *__restrict__ pairs,
-                                                             unsigned int *__restrict__ counter) {
+                                                             int64_t n_chunks, const int32_t *__restrict__ tile_start,
+                                                             uint2 *__restrict__ pairs) {
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ double s_lut[VOCAB];
-    __shared__ int64_t s_unit;
+    __shared__ int64_t s_chunk;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    for (;;) {
+    const int32_t n_tiles = tile_start[n_chunks];
+    for (int32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         __syncthreads();
-        if (threadIdx.x == 0) s_unit = (int64_t)atomicAdd(counter, 1u);
+        if (threadIdx.x == 0) {
+            // last chunk c with tile_start[c] <= tile (chunks without tiles are skipped)
+            int64_t lo = 0, hi = n_chunks - 1;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi + 1) >> 1;
+                if (tile_start[mid] <= tile) lo = mid;
+                else hi = mid - 1;
+            }
+            s_chunk = lo;
+        }
         __syncthreads();
-        const int64_t c = s_unit;
-        if (c >= n_chunks) break;
+        const int64_t c = s_chunk;
         const int32_t L = lengths[c];
+        const int32_t t0 = (tile - tile_start[c]) * R_TILE;
         const uint8_t *tk = tokens + tok_off[c];
         uint2 *out = pairs + tok_off[c];
-        for (int32_t t0 = 0; t0 < L; t0 += R_TILE) {
-            // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
-            for (int i = threadIdx.x; i < R_TILE + WIN; i += THREADS) {
-                const int32_t pos = t0 - WIN + i;
-                s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
+        // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
+        for (int i = threadIdx.x; i < R_TILE + WIN; i += THREADS) {
+            const int32_t pos = t0 - WIN + i;
+            s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
+        }
+        __syncthreads();
+        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
+                                wave, lane);
+        const int32_t valid = min(R_TILE, L - t0);
+        for (int gi = wave; gi * 4 < valid; gi += WAVES) {
+            const int r = gi * 4 + q4;
+            Freq16 fr;
+            row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
+            const int s = s_tok[r + WIN];
+            if (r < valid && (s >> 4) == u) {
+                uint32_t cum, freq;
+                freq16_at(fr, s & 15, cum, freq);
+                out[t0 + r] = make_uint2(cum, freq);
             }
-            __syncthreads();
-            mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
-                                    wave, lane);
-            const int32_t valid = min(R_TILE, L - t0);
-            for (int gi = wave; gi * 4 < valid; gi += WAVES) {
-                const int r = gi * 4 + q4;
-                Freq16 fr;
-                row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
-                const int s = s_tok[r + WIN];
-                if (r < valid && (s >> 4) == u) {
-                    uint32_t cum, freq;
-                    freq16_at(fr, s & 15, cum, freq);
-                    out[t0 + r] = make_uint2(cum, freq);
-                }
-            }
-            __syncthreads();
         }
     }
 }
@@ -188,11 +228,6 @@ __global__ __launch_bounds__(256) void k_encode_pairs(const uint2 *__restrict__ 
     if (!st && L > 0 && enc_seal(s, out, cap)) st = SC_STATUS_CAPACITY;
     word_cnt[c] = s.pos;
     status[c] = st;
-}
-
-__global__ void k_zero_u32(unsigned int *p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
 }
 
 // ---- decompress: persistent autoregressive loop per chunk tile ----------
@@ -293,12 +328,19 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                         s_point[r] = point;
                         s_rpos[r] = rpos;
                         s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
-                        tokens[s_toff[r] + t] = (uint8_t)sym;
                     }
                 }
             }
         }
         __syncthreads();
+        // every 64 steps (and at the end) the ring holds the last 64 tokens
+        // of each chunk: one wavefront per chunk writes them as one 64-byte
+        // run instead of a byte per step
+        if ((t & (WIN - 1)) == WIN - 1 || t == maxlen - 1) {
+            const int32_t p = (t & ~(WIN - 1)) + lane;
+            for (int r = wave; r < R; r += WAVES)
+                if (p <= t && p < s_len[r]) tokens[s_toff[r] + p] = s_ring[r * WIN + lane];
+        }
     }
     for (int r = threadIdx.x; r < R; r += THREADS)
         if (c0 + r < n_chunks) status[c0 + r] = s_stat[r];
@@ -745,10 +787,13 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
     return check_launch("k_decode_step");
 }
 
+// Workspace: tile_start (int32 [n_chunks + 1]), then the (cum, freq) pairs
+// (8 bytes per token), each part 256-byte aligned.
+static int64_t tile_start_bytes(int64_t n_chunks) { return ((n_chunks + 1) * 4 + 255) / 256 * 256; }
+
 int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks) {
-    (void)n_chunks;
-    if (n_tokens < 0) return -1;
-    return 256 + ((n_tokens * 8 + 255) / 256) * 256;
+    if (n_tokens < 0 || n_chunks < 0) return -1;
+    return tile_start_bytes(n_chunks) + ((n_tokens * 8 + 255) / 256) * 256;
 }
 
 int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *tok_off, const int32_t *lengths,
@@ -762,16 +807,19 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
     if (workspace_bytes < sc_compress_workspace_bytes(n_tokens, n_chunks))
         return fail(SC_ERR_ARG, "workspace too small");
     DeviceGuard guard(m->device);
-    unsigned int *counter = (unsigned int *)workspace;
-    uint2 *pairs = (uint2 *)((char *)workspace + 256);
+    if (n_tokens / R_TILE + n_chunks >= (int64_t(1) << 31))
+        return fail(SC_ERR_UNSUPPORTED, "more than 2**31 tiles");
+    int32_t *tile_start = (int32_t *)workspace;
+    uint2 *pairs = (uint2 *)((char *)workspace + tile_start_bytes(n_chunks));
     hipStream_t s = as_stream(stream);
-    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, s, counter, 64);
-    int rc = check_launch("k_zero_u32");
+    hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_THREADS), 0, s, lengths, n_chunks, tile_start);
+    int rc = check_launch("k_tile_scan");
     if (rc) return rc;
-    const int grid = (int)std::min<int64_t>(n_chunks, m->n_cu);
+    // one workgroup per CU (or per tile when there are fewer tiles)
+    const int64_t max_tiles = n_tokens / R_TILE + n_chunks;
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(max_tiles, m->n_cu));
     hipLaunchKernelGGL(m->dev.pipe ? k_compress_mlp<true> : k_compress_mlp<false>, dim3(grid), dim3(THREADS), 0, s,
-                       m->dev, tokens, tok_off, lengths, n_chunks,
-                       pairs, counter);
+                       m->dev, tokens, tok_off, lengths, n_chunks, tile_start, pairs);
     rc = check_launch("k_compress_mlp");
     if (rc) return rc;
     hipLaunchKernelGGL(k_encode_pairs, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, pairs, tok_off,
