@@ -156,10 +156,25 @@ def bench_codec(args):
         "wall_s_timed": round(wall, 3),
         "roofline": {"kernel": "k_decompress", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                     "traffic": None,
+                     "traffic": pmc_traffic(args.config, "k_decompress"),
+                     "traffic_source": f"profiles/traffic_{args.config}.txt (rocprofv3 PMC, bytes per launch)",
                      "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch"},
     }
     return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
+
+
+def pmc_traffic(config, kernel):
+    """HBM-side bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary of this workload (profiles/traffic_<config>.txt: FETCH_SIZE +
+    WRITE_SIZE passes, calibrated against a copy kernel), or None."""
+    path = REPO / "profiles" / f"traffic_{config}.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
+            return int(f[2])
+    return None
 
 
 def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
