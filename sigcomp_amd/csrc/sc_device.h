@@ -590,63 +590,117 @@ __device__ __forceinline__ double row16_sum_f64(double x) {
 // quotients <= 2**24), so floor(q) is exact unless q lies within 2**-20 of
 // an integer; a row with such a value redoes its 16 quotients with the
 // exact integer division (div_floor_est).
-__device__ __forceinline__ void row_frequencies16(v4i raw, const double *s_lut, int u, Freq16 &o) {
-    int l[16];
+//
+// N rows at once (N independent 16-lane rows per lane group): the phases
+// of the N rows are interleaved in straight-line code so their latency
+// chains (LDS lookups, DPP reductions, float64 division) overlap; only the
+// rare exact-division fallback is a branch, taken when any of the N rows
+// needs it.
+template <int N>
+__device__ __forceinline__ void row_frequencies16n(const v4i (&raw)[N], const double *s_lut, int u,
+                                                   Freq16 (&o)[N]) {
+    int l[N][16];
+    int m[N];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) l[k] = (int)(int8_t)((uint32_t)raw[k >> 2] >> (8 * (k & 3)));
-    int lm = l[0];
+    for (int n = 0; n < N; ++n) {
 #pragma unroll
-    for (int k = 1; k < 16; ++k) lm = max(lm, l[k]);
-    const int m = row16_max(lm);
-    double uu[16];
-    double tl = 0.0;
+        for (int k = 0; k < 16; ++k) l[n][k] = (int)(int8_t)((uint32_t)raw[n][k >> 2] >> (8 * (k & 3)));
+        int lm = l[n][0];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        uu[k] = s_lut[m - l[k]];
-        tl += uu[k];
+        for (int k = 1; k < 16; ++k) lm = max(lm, l[n][k]);
+        m[n] = lm;
     }
-    const double T = row16_sum_f64(tl);
-    const double r24 = 16777216.0 / T;
-    bool near = false;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const double q = uu[k] * r24;
-        const double fr = q - __builtin_floor(q);
-        near = near || fr < 0x1p-20 || fr > 1.0 - 0x1p-20;
-        const uint32_t fq = (uint32_t)q;
-        o.f[k] = fq < 1u ? 1u : fq;
-    }
-    if (near) {
-        const uint64_t Ti = (uint64_t)T;
-        const double rT = 1.0 / T;
+    for (int n = 0; n < N; ++n) m[n] = row16_max(m[n]);
+    double uu[N][16];
+    double T[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        double tl = 0.0;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const uint64_t q = div_floor_est(((uint64_t)uu[k]) << 24, Ti, rT);
-            o.f[k] = q < 1 ? 1u : (uint32_t)q;
+            uu[n][k] = s_lut[m[n] - l[n][k]];
+            tl += uu[n][k];
+        }
+        T[n] = tl;
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) T[n] = row16_sum_f64(T[n]);
+    bool near = false;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const double r24 = 16777216.0 / T[n];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const double q = uu[n][k] * r24;
+            const double fr = q - __builtin_floor(q);
+            near = near || fr < 0x1p-20 || fr > 1.0 - 0x1p-20;
+            const uint32_t fq = (uint32_t)q;
+            o[n].f[k] = fq < 1u ? 1u : fq;
         }
     }
-    uint32_t sl = 0, fl = 0;
+    if (near) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        sl += o.f[k];
-        fl = max(fl, o.f[k]);
+        for (int n = 0; n < N; ++n) {
+            const uint64_t Ti = (uint64_t)T[n];
+            const double rT = 1.0 / T[n];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const uint64_t q = div_floor_est(((uint64_t)uu[n][k]) << 24, Ti, rT);
+                o[n].f[k] = q < 1 ? 1u : (uint32_t)q;
+            }
+        }
     }
-    const uint32_t S = row16_sum(sl);
-    const int fm = row16_max((int)fl);
-    int cand = 1 << 20;
+    uint32_t S[N];
+    int fm[N];
 #pragma unroll
-    for (int k = 15; k >= 0; --k)
-        if ((int)o.f[k] == fm) cand = 16 * u + k;
-    const int idx = row16_min(cand);
-    if ((idx >> 4) == u) {
+    for (int n = 0; n < N; ++n) {
+        uint32_t sl = 0, fl = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            sl += o[n].f[k];
+            fl = max(fl, o[n].f[k]);
+        }
+        S[n] = sl;
+        fm[n] = (int)fl;
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        S[n] = row16_sum(S[n]);
+        fm[n] = row16_max(fm[n]);
+    }
+    int idx[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        int cand = 1 << 20;
+#pragma unroll
+        for (int k = 15; k >= 0; --k)
+            if ((int)o[n].f[k] == fm[n]) cand = 16 * u + k;
+        idx[n] = cand;
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) idx[n] = row16_min(idx[n]);
+    uint32_t tot[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const bool mine = (idx[n] >> 4) == u;
 #pragma unroll
         for (int k = 0; k < 16; ++k)
-            if ((idx & 15) == k) o.f[k] -= S - TOTAL;
-    }
-    uint32_t tot = 0;
+            if (mine && (idx[n] & 15) == k) o[n].f[k] -= S[n] - TOTAL;
+        uint32_t t = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) tot += o.f[k];
-    o.ex = row16_excl_scan(tot);
+        for (int k = 0; k < 16; ++k) t += o[n].f[k];
+        tot[n] = t;
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) o[n].ex = row16_excl_scan(tot[n]);
+}
+
+__device__ __forceinline__ void row_frequencies16(v4i raw, const double *s_lut, int u, Freq16 &o) {
+    const v4i r[1] = {raw};
+    Freq16 f[1];
+    row_frequencies16n<1>(r, s_lut, u, f);
+    o = f[0];
 }
 
 // cumulative frequency and frequency of local symbol k (0..15) of this lane

@@ -86,19 +86,25 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
                     *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_at<PIPE>(r, c));
             }
         } else {
-            for (int gi = wave; gi < R_TILE / 4; gi += WAVES) {
-                const int r = gi * 4 + q4;
-                Freq16 fr;
-                row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
-                if (row0 + r < rows) {
-                    int32_t *dst = cdf + (row0 + r) * (VOCAB + 1) + 16 * u;
-                    uint32_t c = fr.ex;
+            // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n
+            for (int gi = wave; gi < R_TILE / 4; gi += 2 * WAVES) {
+                const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
+                const v4i raw[2] = {*(const v4i *)(s_act + act_at<PIPE>(rr[0], u)),
+                                    *(const v4i *)(s_act + act_at<PIPE>(rr[1], u))};
+                Freq16 fr[2];
+                row_frequencies16n<2>(raw, s_lut, u, fr);
 #pragma unroll
-                    for (int k = 0; k < 16; ++k) {
-                        dst[k] = (int32_t)c;
-                        c += fr.f[k];
+                for (int n = 0; n < 2; ++n) {
+                    if (row0 + rr[n] < rows) {
+                        int32_t *dst = cdf + (row0 + rr[n]) * (VOCAB + 1) + 16 * u;
+                        uint32_t c = fr[n].ex;
+#pragma unroll
+                        for (int k = 0; k < 16; ++k) {
+                            dst[k] = (int32_t)c;
+                            c += fr[n].f[k];
+                        }
+                        if (u == 15) dst[16] = (int32_t)TOTAL;
                     }
-                    if (u == 15) dst[16] = (int32_t)TOTAL;
                 }
             }
         }
@@ -187,15 +193,22 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
         mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
                                 wave, lane);
         const int32_t valid = min(R_TILE, L - t0);
-        for (int gi = wave; gi * 4 < valid; gi += WAVES) {
-            const int r = gi * 4 + q4;
-            Freq16 fr;
-            row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
-            const int s = s_tok[r + WIN];
-            if (r < valid && (s >> 4) == u) {
-                uint32_t cum, freq;
-                freq16_at(fr, s & 15, cum, freq);
-                out[t0 + r] = make_uint2(cum, freq);
+        // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n
+        for (int gi = wave; gi * 4 < valid; gi += 2 * WAVES) {
+            const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
+            const v4i raw[2] = {*(const v4i *)(s_act + act_at<PIPE>(rr[0], u)),
+                                *(const v4i *)(s_act + act_at<PIPE>(rr[1], u))};
+            Freq16 fr[2];
+            row_frequencies16n<2>(raw, s_lut, u, fr);
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int r = rr[n];
+                const int s = s_tok[r + WIN];
+                if (r < valid && (s >> 4) == u) {
+                    uint32_t cum, freq;
+                    freq16_at(fr[n], s & 15, cum, freq);
+                    out[t0 + r] = make_uint2(cum, freq);
+                }
             }
         }
     }
@@ -295,38 +308,55 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
                            },
                            wave, lane);
-        for (int gi = wave; gi < R / 4; gi += WAVES) {
-            const int r = gi * 4 + q4;
-            Freq16 fr;
-            row_frequencies16(*(const v4i *)(s_act + act_at<PIPE>(r, u)), s_lut, u, fr);
-            // _decode_partition (cpu_entropy_coding.py:230-266); the 16 lanes
-            // of the row compute the same state, lane u == 0 stores it
-            const bool active = t < s_len[r] && s_stat[r] == 0;
-            uint64_t lower = s_lower[r], range = s_range[r], point = s_point[r];
-            const uint64_t scale = range >> 24;
-            uint32_t q = 0;
-            const bool ok = scale != 0 && dec_quantile(point - lower, scale, q);
-            uint32_t cum, freq;
-            const int sym = dec_symbol16(fr, q, lane, cum, freq);
-            if (active) {
-                if (!ok) {
-                    if (u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
-                } else {
-                    lower += scale * cum;
-                    range = scale * freq;
-                    int32_t rpos = s_rpos[r];
-                    if (range < (1ull << 32)) {
-                        lower <<= 32;
-                        range <<= 32;
-                        point <<= 32;
-                        if (rpos < s_wcnt[r]) point |= words[s_woff[r] + rpos];
-                        rpos += 1;
-                    }
-                    if (u == 0) {
-                        s_lower[r] = lower;
-                        s_range[r] = range;
-                        s_point[r] = point;
-                        s_rpos[r] = rpos;
+        // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n.
+        // _decode_partition (cpu_entropy_coding.py:230-266): the 16 lanes of a
+        // row compute the same state, lane u == 0 stores it.  The word a
+        // renormalisation would shift in is loaded before the frequency work
+        // (whether or not this step needs it) so its latency is hidden.
+        for (int gi = wave; gi < R / 4; gi += 2 * WAVES) {
+            const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
+            uint64_t lower[2], range[2], point[2];
+            int32_t rpos[2];
+            uint32_t wnext[2];
+            bool active[2];
+            v4i raw[2];
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int r = rr[n];
+                active[n] = t < s_len[r] && s_stat[r] == 0;
+                lower[n] = s_lower[r];
+                range[n] = s_range[r];
+                point[n] = s_point[r];
+                rpos[n] = s_rpos[r];
+                wnext[n] = rpos[n] < s_wcnt[r] ? words[s_woff[r] + rpos[n]] : 0u;
+                raw[n] = *(const v4i *)(s_act + act_at<PIPE>(r, u));
+            }
+            Freq16 fr[2];
+            row_frequencies16n<2>(raw, s_lut, u, fr);
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int r = rr[n];
+                const uint64_t scale = range[n] >> 24;
+                uint32_t q = 0;
+                const bool ok = scale != 0 && dec_quantile(point[n] - lower[n], scale, q);
+                uint32_t cum, freq;
+                const int sym = dec_symbol16(fr[n], q, lane, cum, freq);
+                if (active[n] && u == 0) {
+                    if (!ok) {
+                        s_stat[r] = SC_STATUS_INVALID_STREAM;
+                    } else {
+                        uint64_t lo = lower[n] + scale * cum, ra = scale * freq, pt = point[n];
+                        int32_t rp = rpos[n];
+                        if (ra < (1ull << 32)) {
+                            lo <<= 32;
+                            ra <<= 32;
+                            pt = (pt << 32) | wnext[n];
+                            rp += 1;
+                        }
+                        s_lower[r] = lo;
+                        s_range[r] = ra;
+                        s_point[r] = pt;
+                        s_rpos[r] = rp;
                         s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
                     }
                 }
