@@ -47,7 +47,7 @@ def build_workload(cfg_name, n_reads):
     cfg = synth.CONFIGS[cfg_name]
     reads = synth.synth_reads(n_reads or cfg["n_reads"], cfg["seed"], cfg["profile"])
     samples = int(sum(len(r) for r in reads))
-    small = [signal.split_signal(signal.prepare_signal(r, cfg["lsb"]))[1] for r in reads]
+    small = signal.reads_tokens(signal.split_reads(reads, cfg["lsb"]))
     chunks = [s[i:i + CHUNK_LEN] for s in small for i in range(0, len(s), CHUNK_LEN)]
     return cfg, reads, samples, small, chunks
 

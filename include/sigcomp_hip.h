@@ -175,6 +175,14 @@ int sc_compress_chunks(const sc_model *model, const uint8_t *tokens, const int64
                        int32_t *word_cnt, int32_t *status, void *workspace,
                        int64_t workspace_bytes, void *stream);
 
+/* Copy each chunk's word_cnt[c] words from words + word_off[c] to
+ * out + out_off[c] (device arrays), e.g. from sc_compress_chunks' capacity
+ * slots into a dense buffer before the device -> host copy.  Replaces the
+ * full-buffer transfer of GpuRangeStepEncoder.get_compressed
+ * (gpu_entropy_coding.py:292-303). */
+int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt, int64_t n_chunks,
+                    uint32_t *out, const int64_t *out_off, void *stream);
+
 /* Decompress n_chunks chunks with one persistent kernel: every workgroup owns
  * a tile of chunks and runs the whole autoregressive loop for them (MLP step,
  * fused frequency step and decoder step per token, context kept on chip).

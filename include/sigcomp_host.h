@@ -1,0 +1,104 @@
+/*
+ * sigcomp_host.h -- C ABI of the host-side stages either side of the GPU
+ * codec: signal split / reassembly (the caller-side token source) and the
+ * SIG2 per-chunk framing.  libsigcomp_host.so, plain C++ on the CPU,
+ * multithreaded over reads / chunks.  Every function names the reference
+ * code it restates (paths relative to the reference's sigcomp/ package).
+ *
+ * Conventions: all pointers are host pointers, read or written during the
+ * call only.  Input reads are given as an array of per-read pointers plus
+ * lengths; other per-item data as concatenated arrays plus per-item offsets
+ * and lengths.  n_threads <= 0 uses every hardware thread.
+ * Return value: SC_OK; SC_ERR_ARG for bad arguments; or an SC_HOST_ERR_*
+ * code with *bad set to the index of the first (lowest-numbered) offending
+ * item (when `bad` is not NULL); sc_host_last_error() describes the
+ * failure.  Items are independent, so a failing item leaves
+ * the outputs of other items valid.
+ */
+#ifndef SIGCOMP_HOST_H
+#define SIGCOMP_HOST_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifndef SC_OK
+#define SC_OK 0
+#define SC_ERR_ARG 1
+#endif
+
+/* Item failures (the reference's exception for each, as raised by the Python
+ * layer, in brackets). */
+#define SC_HOST_ERR_FRAME_LENGTH 10  /* truncated uint16 frame length [ValueError] */
+#define SC_HOST_ERR_FRAME        11  /* empty, non-multiple-of-4 or truncated frame [ValueError] */
+#define SC_HOST_ERR_TRAILING     12  /* bytes after the last frame [ValueError] */
+#define SC_HOST_ERR_OVERSIZE     13  /* chunk of more than 65535 bytes [ValueError] */
+#define SC_HOST_ERR_COUNTS       14  /* small + large counts != len - 1 [ValueError] */
+#define SC_HOST_ERR_POSITION     15  /* large position outside the read [IndexError] */
+#define SC_HOST_ERR_EMPTY_READ   16  /* a read of zero samples [IndexError] */
+
+const char *sc_host_last_error(void);
+
+/* Pass 1 of the split.  For each read r (len[r] >= 1 samples at reads[r]):
+ * apply the lossy transform when lsb > 0
+ * (_lossy_encode(_reduce_lsb(sig, lsb), lsb), main.py:158-167,862-864), then
+ * count the small (zigzag delta < 256) and large deltas of _split_signal
+ * (main.py:504-521).  Writes sig0[r] (first transformed sample),
+ * n_small[r], n_large[r] (n_small + n_large = len - 1).  lsb in [0, 15]. */
+int sc_host_split_count(const int16_t *const *reads, const int64_t *len, int64_t n_reads, int32_t lsb,
+                        int16_t *sig0, int64_t *n_small, int64_t *n_large, int32_t n_threads, int64_t *bad);
+
+/* Pass 2 of the split: read r's small tokens (uint8, in order) go to
+ * small + small_off[r], its large values minus 256 (uint16) to
+ * large_adj + large_off[r] and the gap-coded positions (first position,
+ * then position differences minus one; uint32) to large_gap + large_off[r].
+ * Offsets are the caller's (normally exclusive scans of n_small / n_large). */
+int sc_host_split_fill(const int16_t *const *reads, const int64_t *len, int64_t n_reads, int32_t lsb,
+                       const int64_t *small_off, const int64_t *large_off, uint8_t *small, uint16_t *large_adj,
+                       uint32_t *large_gap, int32_t n_threads, int64_t *bad);
+
+/* Inverse (_reassemble_signal, main.py:524-546, after the Rice decoding of
+ * the large values and gaps; then _lossy_decode, main.py:170-171,1164 when
+ * lsb > 0): read r (len[r] samples, first sig0[r]) from n_small[r] tokens at
+ * small + small_off[r] and n_large[r] large values / gaps at large_off[r];
+ * samples to out + out_off[r].  Fails for a read whose counts do not add up
+ * to len - 1 or whose positions fall outside the read (the reference raises
+ * IndexError / ValueError there). */
+int sc_host_reassemble(const int16_t *sig0, const int64_t *len, int64_t n_reads, int32_t lsb,
+                       const uint8_t *small, const int64_t *small_off, const int64_t *n_small,
+                       const uint16_t *large_adj, const uint32_t *large_gap, const int64_t *large_off,
+                       const int64_t *n_large, int16_t *out, const int64_t *out_off, int32_t n_threads,
+                       int64_t *bad);
+
+/* SIG2 framing of range-coded chunks (ReadFramingMixin.batch_inference_reads,
+ * cpu_compression.py:44-52): chunk c = word_cnt[c] little-endian u32 words at
+ * words + word_off[c]; its frame (a little-endian uint16 byte length, then the
+ * words) goes to out + out_off[c].  A read's payload is the concatenation of
+ * its chunks' frames, so out_off is the exclusive scan of 2 + 4*word_cnt.
+ * Fails for a chunk of more than 65535 bytes. */
+int sc_host_frame(const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt, int64_t n_chunks,
+                  uint8_t *out, const int64_t *out_off, int32_t n_threads, int64_t *bad);
+
+/* Parse framed reads (cpu_compression.py:60-84): read r's payload is
+ * data[data_off[r] .. data_off[r] + data_len[r]) and holds
+ * ceil(tokens[r] / chunk_len) frames, chunk k of it covering
+ * min(chunk_len, tokens[r] - k*chunk_len) tokens.  Its chunks are numbered
+ * from chunk_begin[r] (the caller's exclusive scan of the frame counts) and
+ * their words are copied, in order, to words_out from read_word_off[r] on
+ * (data_len[r] / 4 words of room per read always suffice); for each chunk c,
+ * word_off[c] (absolute index into words_out), word_cnt[c] and tok_cnt[c] are
+ * written.  Fails for a frame of zero bytes or of a byte count that is not a
+ * multiple of four, a truncated frame, or trailing bytes after the last
+ * frame. */
+int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *data_len, const int64_t *tokens,
+                  int64_t n_reads, int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off,
+                  uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,
+                  int64_t *bad);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIGCOMP_HOST_H */

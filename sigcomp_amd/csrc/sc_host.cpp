@@ -1,0 +1,291 @@
+// sc_host.cpp -- host stages either side of the GPU codec (C ABI in
+// include/sigcomp_host.h): signal split / reassembly and SIG2 chunk framing,
+// multithreaded over reads or chunks.
+#include "../../include/sigcomp_host.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+// Runs f(i) for i in [0, n) on up to n_threads threads (dynamic blocks of
+// indices); returns after every call ended.
+template <class F>
+void parallel_for(int64_t n, int32_t n_threads, F f) {
+    int64_t hw = (int64_t)std::thread::hardware_concurrency();
+    int64_t nt = n_threads > 0 ? n_threads : std::max<int64_t>(hw, 1);
+    nt = std::min<int64_t>(nt, std::max<int64_t>(n / 16, 1));
+    if (nt <= 1) {
+        for (int64_t i = 0; i < n; ++i) f(i);
+        return;
+    }
+    const int64_t block = std::max<int64_t>(1, n / (nt * 8));
+    std::atomic<int64_t> next{0};
+    auto worker = [&]() {
+        for (;;) {
+            const int64_t b = next.fetch_add(block);
+            if (b >= n) break;
+            const int64_t e = std::min(n, b + block);
+            for (int64_t i = b; i < e; ++i) f(i);
+        }
+    };
+    std::vector<std::thread> pool;
+    pool.reserve((size_t)nt - 1);
+    for (int64_t t = 1; t < nt; ++t) pool.emplace_back(worker);
+    worker();
+    for (auto &th : pool) th.join();
+}
+
+// First (lowest-numbered) failing item over all threads.
+struct FirstBad {
+    std::mutex m;
+    int64_t idx = INT64_MAX;
+    int code = SC_OK;
+    void report(int64_t i, int c) {
+        std::lock_guard<std::mutex> g(m);
+        if (i < idx) {
+            idx = i;
+            code = c;
+        }
+    }
+};
+
+const char *err_text(int code) {
+    switch (code) {
+        case SC_HOST_ERR_FRAME_LENGTH: return "Truncated SIG2 chunk length";
+        case SC_HOST_ERR_FRAME: return "Invalid or truncated SIG2 range-coded chunk";
+        case SC_HOST_ERR_TRAILING: return "Trailing SIG2 chunk data disagrees with token length";
+        case SC_HOST_ERR_OVERSIZE: return "Compressed chunk exceeds the SIG2 uint16 frame";
+        case SC_HOST_ERR_COUNTS: return "small and large value counts disagree with the read length";
+        case SC_HOST_ERR_POSITION: return "large-value position outside the read";
+        case SC_HOST_ERR_EMPTY_READ: return "a read has no samples";
+        default: return "error";
+    }
+}
+
+int finish(FirstBad &fb, int64_t *bad) {
+    if (fb.idx == INT64_MAX) return SC_OK;
+    if (bad) *bad = fb.idx;
+    g_err = std::string(err_text(fb.code)) + " (item " + std::to_string(fb.idx) + ")";
+    return fb.code;
+}
+
+// _reduce_lsb then _lossy_encode (main.py:158-167) on one sample, int16 wrap
+inline int16_t lossy_sample(int16_t s, int lsb) {
+    if (lsb <= 0) return s;
+    const int32_t v = s;
+    const int32_t step = 1 << lsb;
+    const int32_t rounding = ((v >> (lsb - 1)) & 1) * step;
+    const int32_t upper = v & ~(step - 1);
+    const int16_t reduced = (int16_t)(uint16_t)(uint32_t)(upper + rounding);
+    return (int16_t)(uint16_t)(uint32_t)((int32_t)reduced >> lsb);
+}
+
+// zigzag of the int16 delta b - a (np.diff on int16 wraps modulo 2**16)
+inline uint16_t zz_delta(int16_t a, int16_t b) {
+    const int32_t d = (int16_t)(uint16_t)((uint32_t)(uint16_t)b - (uint32_t)(uint16_t)a);
+    return (uint16_t)(uint32_t)((d << 1) ^ (d >> 31));
+}
+
+inline int16_t unzigzag(uint16_t z) {
+    const uint32_t v = z;
+    return (int16_t)(uint16_t)((v >> 1) ^ (0u - (v & 1u)));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *sc_host_last_error(void) { return g_err.c_str(); }
+
+int sc_host_split_count(const int16_t *const *reads, const int64_t *len, int64_t n_reads, int32_t lsb,
+                        int16_t *sig0, int64_t *n_small, int64_t *n_large, int32_t n_threads, int64_t *bad) {
+    if (n_reads < 0 || lsb < 0 || lsb > 15 || (n_reads && (!reads || !len || !sig0 || !n_small || !n_large))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_reads, n_threads, [&](int64_t r) {
+        const int64_t n = len[r];
+        if (n < 1) {
+            fb.report(r, SC_HOST_ERR_EMPTY_READ);
+            return;
+        }
+        const int16_t *s = reads[r];
+        int16_t prev = lossy_sample(s[0], lsb);
+        int64_t small = 0;
+        for (int64_t i = 1; i < n; ++i) {
+            const int16_t cur = lossy_sample(s[i], lsb);
+            small += zz_delta(prev, cur) < 256;
+            prev = cur;
+        }
+        sig0[r] = lossy_sample(s[0], lsb);
+        n_small[r] = small;
+        n_large[r] = n - 1 - small;
+    });
+    return finish(fb, bad);
+}
+
+int sc_host_split_fill(const int16_t *const *reads, const int64_t *len, int64_t n_reads, int32_t lsb,
+                       const int64_t *small_off, const int64_t *large_off, uint8_t *small, uint16_t *large_adj,
+                       uint32_t *large_gap, int32_t n_threads, int64_t *bad) {
+    if (n_reads < 0 || lsb < 0 || lsb > 15 ||
+        (n_reads && (!reads || !len || !small_off || !large_off || !small || !large_adj || !large_gap))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_reads, n_threads, [&](int64_t r) {
+        const int64_t n = len[r];
+        if (n < 1) {
+            fb.report(r, SC_HOST_ERR_EMPTY_READ);
+            return;
+        }
+        const int16_t *s = reads[r];
+        uint8_t *sm = small + small_off[r];
+        uint16_t *la = large_adj + large_off[r];
+        uint32_t *lg = large_gap + large_off[r];
+        int16_t prev = lossy_sample(s[0], lsb);
+        int64_t last = -1;   // position of the previous large value
+        for (int64_t i = 1; i < n; ++i) {
+            const int16_t cur = lossy_sample(s[i], lsb);
+            const uint16_t z = zz_delta(prev, cur);
+            prev = cur;
+            if (z < 256) {
+                *sm++ = (uint8_t)z;
+            } else {
+                const int64_t pos = i - 1;
+                *la++ = (uint16_t)(z - 256);
+                *lg++ = (uint32_t)(last < 0 ? pos : pos - last - 1);
+                last = pos;
+            }
+        }
+    });
+    return finish(fb, bad);
+}
+
+int sc_host_reassemble(const int16_t *sig0, const int64_t *len, int64_t n_reads, int32_t lsb, const uint8_t *small,
+                       const int64_t *small_off, const int64_t *n_small, const uint16_t *large_adj,
+                       const uint32_t *large_gap, const int64_t *large_off, const int64_t *n_large, int16_t *out,
+                       const int64_t *out_off, int32_t n_threads, int64_t *bad) {
+    if (n_reads < 0 || lsb < 0 || lsb > 15 ||
+        (n_reads && (!sig0 || !len || !small_off || !n_small || !large_off || !n_large || !out || !out_off))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_reads, n_threads, [&](int64_t r) {
+        const int64_t n = len[r];
+        if (n < 1) {
+            fb.report(r, SC_HOST_ERR_EMPTY_READ);
+            return;
+        }
+        if (n_small[r] < 0 || n_large[r] < 0 || n_small[r] + n_large[r] != n - 1) {
+            fb.report(r, SC_HOST_ERR_COUNTS);
+            return;
+        }
+        const uint8_t *sm = small + small_off[r];
+        const uint16_t *la = large_adj + large_off[r];
+        const uint32_t *lg = large_gap + large_off[r];
+        // positions: first gap, then gap + 1 steps; strictly increasing
+        int64_t next_large = n_large[r] ? (int64_t)lg[0] : INT64_MAX, k = 0;
+        if (n_large[r] && next_large >= n - 1) {
+            fb.report(r, SC_HOST_ERR_POSITION);
+            return;
+        }
+        int16_t *o = out + out_off[r];
+        int16_t v = sig0[r];
+        o[0] = lsb ? (int16_t)(uint16_t)(uint32_t)((int32_t)v << lsb) : v;
+        int64_t js = 0;
+        for (int64_t i = 0; i < n - 1; ++i) {
+            uint16_t z;
+            if (i == next_large) {
+                z = (uint16_t)(la[k] + 256u);
+                ++k;
+                if (k < n_large[r]) {
+                    next_large += (int64_t)lg[k] + 1;
+                    if (next_large >= n - 1) {
+                        fb.report(r, SC_HOST_ERR_POSITION);
+                        return;
+                    }
+                }
+            } else {
+                z = sm[js++];
+            }
+            v = (int16_t)(uint16_t)((uint32_t)(uint16_t)v + (uint32_t)(uint16_t)unzigzag(z));
+            o[i + 1] = lsb ? (int16_t)(uint16_t)(uint32_t)((int32_t)v << lsb) : v;
+        }
+    });
+    return finish(fb, bad);
+}
+
+int sc_host_frame(const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt, int64_t n_chunks,
+                  uint8_t *out, const int64_t *out_off, int32_t n_threads, int64_t *bad) {
+    if (n_chunks < 0 || (n_chunks && (!words || !word_off || !word_cnt || !out || !out_off))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_chunks, n_threads, [&](int64_t c) {
+        const int64_t bytes = (int64_t)word_cnt[c] * 4;
+        if (word_cnt[c] < 0 || bytes > 65535) {
+            fb.report(c, SC_HOST_ERR_OVERSIZE);
+            return;
+        }
+        uint8_t *o = out + out_off[c];
+        o[0] = (uint8_t)(bytes & 0xFF);
+        o[1] = (uint8_t)(bytes >> 8);
+        std::memcpy(o + 2, words + word_off[c], (size_t)bytes);   // little-endian host
+    });
+    return finish(fb, bad);
+}
+
+int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *data_len, const int64_t *tokens,
+                  int64_t n_reads, int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off,
+                  uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,
+                  int64_t *bad) {
+    if (n_reads < 0 || chunk_len < 1 ||
+        (n_reads && (!data_off || !data_len || !tokens || !chunk_begin || !read_word_off || !word_off ||
+                     !word_cnt || !tok_cnt))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_reads, n_threads, [&](int64_t r) {
+        const uint8_t *d = data + data_off[r];
+        const int64_t size = data_len[r];
+        int64_t remaining = tokens[r], pos = 0, c = chunk_begin[r], w = read_word_off[r];
+        while (remaining > 0) {
+            if (pos + 2 > size) {
+                fb.report(r, SC_HOST_ERR_FRAME_LENGTH);
+                return;
+            }
+            const int64_t fbytes = (int64_t)d[pos] | ((int64_t)d[pos + 1] << 8);
+            pos += 2;
+            if (fbytes == 0 || fbytes % 4 || pos + fbytes > size) {
+                fb.report(r, SC_HOST_ERR_FRAME);
+                return;
+            }
+            const int64_t count = std::min<int64_t>(chunk_len, remaining);
+            std::memcpy(words_out + w, d + pos, (size_t)fbytes);
+            word_off[c] = w;
+            word_cnt[c] = (int32_t)(fbytes / 4);
+            tok_cnt[c] = (int32_t)count;
+            w += fbytes / 4;
+            pos += fbytes;
+            remaining -= count;
+            ++c;
+        }
+        if (pos != size) fb.report(r, SC_HOST_ERR_TRAILING);
+    });
+    return finish(fb, bad);
+}
+
+}  // extern "C"

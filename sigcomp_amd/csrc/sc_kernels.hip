@@ -376,6 +376,24 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         if (c0 + r < n_chunks) status[c0 + r] = s_stat[r];
 }
 
+// ---- word compaction -----------------------------------------------------
+
+// One wavefront per chunk copies its word_cnt[c] words from its capacity slot
+// to out + out_off[c] (coalesced 4-byte lanes).
+__global__ __launch_bounds__(256) void k_gather_words(const uint32_t *__restrict__ words,
+                                                      const int64_t *__restrict__ word_off,
+                                                      const int32_t *__restrict__ word_cnt, int64_t n_chunks,
+                                                      uint32_t *__restrict__ out,
+                                                      const int64_t *__restrict__ out_off) {
+    const int64_t c = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+    if (c >= n_chunks) return;
+    const int lane = threadIdx.x & 63;
+    const uint32_t *src = words + word_off[c];
+    uint32_t *dst = out + out_off[c];
+    const int32_t n = word_cnt[c];
+    for (int32_t i = lane; i < n; i += 64) dst[i] = src[i];
+}
+
 // ---- step-API kernels (GpuRangeStepEncoder / GpuRangeDecoder) ------------
 // 256 threads = 16 rows per workgroup (four 16-lane rows per wavefront).
 
@@ -855,6 +873,16 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
     hipLaunchKernelGGL(k_encode_pairs, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, pairs, tok_off,
                        lengths, n_chunks, words, word_off, word_cap, word_cnt, status);
     return check_launch("k_encode_pairs");
+}
+
+int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt, int64_t n_chunks,
+                    uint32_t *out, const int64_t *out_off, void *stream) {
+    if (n_chunks < 0) return fail(SC_ERR_ARG, "bad argument");
+    if (n_chunks == 0) return SC_OK;
+    if (!words || !word_off || !word_cnt || !out || !out_off) return fail(SC_ERR_ARG, "null device pointer");
+    hipLaunchKernelGGL(k_gather_words, dim3((unsigned)((n_chunks + WAVES - 1) / WAVES)), dim3(THREADS), 0,
+                       as_stream(stream), words, word_off, word_cnt, n_chunks, out, out_off);
+    return check_launch("k_gather_words");
 }
 
 int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt,

@@ -69,14 +69,22 @@ def parse_framed(data: bytes, length: int, chunk_len: int):
 
 class ReadFramingMixin:
     """Drop-in for the reference mixin: ``batch_inference_reads`` on top of
-    ``self.compress_chunks`` / ``self.decompress_chunks`` and ``self.chunk_len``."""
+    ``self.compress_chunks`` / ``self.decompress_chunks`` and ``self.chunk_len``.
+
+    Codecs that also provide ``compress_flat`` / ``decompress_flat`` (the GPU
+    codec does) take the batched path: chunking, framing and parsing of all
+    reads in one call each to the host library (``sigcomp_amd._host``), with
+    the same bytes and the same errors."""
 
     def batch_inference_reads(self, list_of_reads=None, list_of_compressed_reads=None,
                               list_of_lengths=None, batch_size=64, use_tqdm=False, prob_quant=0):
         if batch_size < 1:
             raise ValueError("batch_size must be positive")
+        flat = hasattr(self, "compress_flat") and hasattr(self, "decompress_flat")
         chunks, lengths, mapping = [], [], []
         if list_of_reads is not None:
+            if flat:
+                return self._compress_reads_flat(list_of_reads, batch_size)
             for read in list_of_reads:
                 begin = len(chunks)
                 chunks.extend(split_into_chunks(read, self.chunk_len))
@@ -88,6 +96,8 @@ class ReadFramingMixin:
             raise ValueError("Compressed reads and token lengths are required")
         if len(list_of_compressed_reads) != len(list_of_lengths):
             raise ValueError("Compressed read and token length counts differ")
+        if flat:
+            return self._decompress_reads_flat(list_of_compressed_reads, list_of_lengths)
         for data, length in zip(list_of_compressed_reads, list_of_lengths):
             begin = len(chunks)
             parts, counts = parse_framed(data, length, self.chunk_len)
@@ -98,3 +108,38 @@ class ReadFramingMixin:
                                          use_tqdm=use_tqdm)
         return [np.concatenate(decoded[b:e]) if e > b else np.empty(0, dtype=np.uint8)
                 for b, e in mapping]
+
+    def _compress_reads_flat(self, list_of_reads, batch_size):
+        from . import _host
+        reads = [as_symbols(r) for r in list_of_reads]
+        cl = int(self.chunk_len)
+        lens = np.fromiter((len(r) for r in reads), np.int64, count=len(reads))
+        nch = (lens + cl - 1) // cl
+        chunk_begin = np.zeros(len(reads) + 1, np.int64)
+        np.cumsum(nch, out=chunk_begin[1:])
+        n_chunks = int(chunk_begin[-1])
+        chunk_len = np.full(n_chunks, cl, np.int32)
+        last = chunk_begin[1:][nch > 0] - 1
+        chunk_len[last] = (lens[nch > 0] - (nch[nch > 0] - 1) * cl).astype(np.int32)
+        tokens = np.concatenate(reads) if reads else np.zeros(0, np.uint8)
+        words, word_off, word_cnt = self.compress_flat(tokens, chunk_len, batch_size)
+        buf, bounds = _host.frame(words, word_off, word_cnt)
+        return [buf[bounds[chunk_begin[r]]:bounds[chunk_begin[r + 1]]].tobytes() for r in range(len(reads))]
+
+    def _decompress_reads_flat(self, payloads, list_of_lengths):
+        from . import _host
+        bad_len = next((i for i, x in enumerate(list_of_lengths) if int(x) != x or x < 0), None)
+        if bad_len is not None:
+            # the reference checks reads in order: a framing error of an
+            # earlier read is raised first
+            _host.parse(payloads[:bad_len], [int(x) for x in list_of_lengths[:bad_len]], int(self.chunk_len))
+            raise ValueError("Token lengths must be nonnegative integers")
+        tokens = np.fromiter((int(x) for x in list_of_lengths), np.int64, count=len(list_of_lengths))
+        pr = _host.parse(payloads, tokens, int(self.chunk_len))
+        tok, tok_off = self.decompress_flat(pr["words"], pr["word_off"], pr["word_cnt"], pr["tok_cnt"])
+        out = []
+        for r, n in enumerate(tokens):
+            c = pr["chunk_begin"][r]
+            start = tok_off[c] if pr["frames"][r] else 0
+            out.append(tok[start:start + n] if n else np.empty(0, dtype=np.uint8))
+        return out

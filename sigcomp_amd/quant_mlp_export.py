@@ -159,41 +159,77 @@ class QuantMLPCompression(ReadFramingMixin):
         chunks = [as_symbols(c) for c in chunks]
         if any(len(c) > self.chunk_len for c in chunks):
             raise ValueError("A token chunk exceeds chunk_len")
-        per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
-        out = []
-        for s in range(0, len(chunks), per):
-            out.extend(self._compress_batch(chunks[s:s + per]))
-        return out
-
-    def _compress_batch(self, chunks):
         n = len(chunks)
         if n == 0:
             return []
         lengths = np.fromiter((len(c) for c in chunks), dtype=np.int32, count=n)
+        tokens = np.concatenate(chunks)
+        words, word_off, word_cnt = self.compress_flat(tokens, lengths, max_batch_size)
+        return [words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in range(n)]
+
+    def compress_flat(self, tokens, lengths, max_batch_size=64):
+        """Compress chunks given as concatenated uint8 tokens and int32 chunk
+        lengths -> (uint32 words of all chunks, densely packed, per-chunk
+        word offsets, per-chunk word counts).  Each chunk is coded
+        independently; launches cover up to max(max_batch_size, 65536)
+        chunks."""
+        tokens = np.ascontiguousarray(tokens, np.uint8)
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        if np.any(lengths < 0) or np.any(lengths > self.chunk_len):
+            raise ValueError("Chunk lengths must be in [0, chunk_len]")
+        if int(lengths.sum()) != len(tokens):
+            raise ValueError("Chunk lengths do not add up to the token count")
+        if len(lengths) == 0:
+            return np.zeros(0, np.uint32), np.zeros(0, np.int64), np.zeros(0, np.int32)
+        per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
+        parts, tok0 = [], 0
+        for s in range(0, len(lengths), per):
+            ln = lengths[s:s + per]
+            nt = int(ln.sum())
+            parts.append(self._compress_batch(tokens[tok0:tok0 + nt], ln))
+            tok0 += nt
+        if len(parts) == 1:
+            return parts[0]
+        words = np.concatenate([p[0] for p in parts])
+        base = np.cumsum([0] + [len(p[0]) for p in parts[:-1]])
+        word_off = np.concatenate([p[1] + b for p, b in zip(parts, base)])
+        return words, word_off, np.concatenate([p[2] for p in parts])
+
+    def _compress_batch(self, tokens, lengths):
+        n = len(lengths)
         tok_off = np.zeros(n, dtype=np.int64)
         np.cumsum(lengths[:-1], out=tok_off[1:])
         n_tokens = int(lengths.sum())
-        tokens = np.concatenate(chunks) if n_tokens else np.zeros(1, np.uint8)
+        if n_tokens == 0:
+            tokens = np.zeros(1, np.uint8)
         cap = lengths + 2
         word_off = np.zeros(n, dtype=np.int64)
         np.cumsum(cap[:-1], dtype=np.int64, out=word_off[1:])
         dev = self.hip.device
-        d = lambda a: torch.from_numpy(a).to(dev, non_blocking=False)
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, non_blocking=False)
         t_tokens, t_tok_off, t_len = d(tokens), d(tok_off), d(lengths)
         t_word_off, t_cap = d(word_off), d(cap.astype(np.int32))
         words, cnt, status, ws = self._compress_buffers(n, n_tokens, int(cap.sum()))
+        L = _hip.lib()
         with torch.cuda.device(dev):
-            _hip.check(_hip.lib().sc_compress_chunks(
+            _hip.check(L.sc_compress_chunks(
                 self.hip.handle, _hip.ptr(t_tokens), _hip.ptr(t_tok_off), _hip.ptr(t_len), n,
                 n_tokens, _hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(t_cap), _hip.ptr(cnt),
                 _hip.ptr(status), _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
-        st = status.cpu().numpy()
-        if st.any():
-            b = int(np.flatnonzero(st)[0])
-            raise OverflowError(f"range-coder output capacity exceeded in stream {b}")
-        cnt_np = cnt.cpu().numpy()
-        words_np = words.cpu().numpy()
-        return [words_np[word_off[i]:word_off[i] + cnt_np[i]].tobytes() for i in range(n)]
+            st = status.cpu().numpy()
+            if st.any():
+                b = int(np.flatnonzero(st)[0])
+                raise OverflowError(f"range-coder output capacity exceeded in stream {b}")
+            # pack the used words densely on the device, then one transfer
+            cnt_np = cnt.cpu().numpy()
+            dense_off = np.zeros(n, dtype=np.int64)
+            np.cumsum(cnt_np[:-1], dtype=np.int64, out=dense_off[1:])
+            dense = torch.empty(max(int(cnt_np.sum()), 1), dtype=torch.int32, device=dev)
+            t_dense_off = d(dense_off)
+            _hip.check(L.sc_gather_words(_hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(cnt), n,
+                                         _hip.ptr(dense), _hip.ptr(t_dense_off), _hip.stream_ptr()))
+            words_np = dense.cpu().numpy().view(np.uint32)
+        return words_np, dense_off, cnt_np
 
     def _compress_buffers(self, n, n_tokens, n_words):
         dev = self.hip.device
@@ -234,15 +270,41 @@ class QuantMLPCompression(ReadFramingMixin):
         np.cumsum(cnt[:-1], dtype=np.int64, out=word_off[1:])
         flat = (np.frombuffer(b"".join(chunk_bytes), dtype="<u4").astype(np.uint32, copy=False)
                 if cnt.sum() else np.zeros(1, np.uint32))
+        tok, tok_off = self.decompress_flat(flat, word_off, cnt, lengths)
+        return [tok[tok_off[i]:tok_off[i] + lengths[i]].copy() for i in range(n)]
+
+    def decompress_flat(self, words, word_off, word_cnt, lengths):
+        """Decompress chunks given as one uint32 word array with per-chunk
+        word offsets / counts and token lengths -> (uint8 tokens of all
+        chunks concatenated in chunk order, per-chunk token offsets).  One
+        persistent-kernel call for all chunks; raises ValueError on a corrupt
+        stream."""
+        words = np.ascontiguousarray(words, np.uint32)
+        word_off = np.ascontiguousarray(word_off, np.int64)
+        cnt = np.ascontiguousarray(word_cnt, np.int32)
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        n = len(lengths)
+        if len(word_off) != n or len(cnt) != n:
+            raise ValueError("Compressed chunk and length counts differ")
+        if n and (np.any(lengths < 0) or np.any(lengths > self.chunk_len)):
+            raise ValueError("Chunk lengths must be integers in [0, chunk_len]")
+        if n and (np.any(word_off < 0) or np.any(word_off + cnt > len(words))
+                  or np.any((lengths > 0) & (cnt == 0)) or np.any((lengths == 0) & (cnt > 0))):
+            raise ValueError("Invalid range-coded chunk for its token length")
         tok_off = np.zeros(n, dtype=np.int64)
-        np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
+        if n > 1:
+            np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
         n_tokens = int(lengths.sum())
+        if n == 0:
+            return np.zeros(0, np.uint8), tok_off
+        if len(words) == 0:
+            words = np.zeros(1, np.uint32)
         # longest chunks first: every workgroup then holds chunks of similar
         # length and stops at its own longest one
         order = np.argsort(-lengths, kind="stable")
         dev = self.hip.device
         d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-        t_words = d(flat.view(np.int32))
+        t_words = d(words.view(np.int32))
         t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(lengths[order]), d(tok_off[order])
         tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)
         status = torch.empty(n, dtype=torch.int32, device=dev)
@@ -255,5 +317,4 @@ class QuantMLPCompression(ReadFramingMixin):
         if st.any():
             raise ValueError("invalid range stream or mismatching entropy model in chunk "
                              f"{int(order[np.flatnonzero(st)[0]])}")
-        tok = tokens.cpu().numpy()
-        return [tok[tok_off[i]:tok_off[i] + lengths[i]].copy() for i in range(n)]
+        return tokens.cpu().numpy()[:n_tokens], tok_off

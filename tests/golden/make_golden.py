@@ -34,8 +34,10 @@ import torch
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parents[1]
 sys.path.insert(0, str(REPO))
+sys.path.insert(0, str(REPO / "oracle"))
 
-from sigcomp_amd import signal, synth  # noqa: E402
+import signal_ref as signal  # noqa: E402  (numpy restatement of main.py's transforms)
+from sigcomp_amd import synth  # noqa: E402
 
 SOS = 256
 WINDOW = 64

@@ -131,7 +131,7 @@ def test_batch_inference_reads_matches_reference_e2e(codecs, name):
     z = np.load(GOLDEN / "e2e_reads.npz")
     lsb = int(z[f"{name}_lsb"])
     n = int(z[f"{name}_nreads"])
-    small = [signal.split_signal(signal.prepare_signal(z[f"{name}_read{i}_signal"], lsb))[1]
+    small = [signal.split_signal(z[f"{name}_read{i}_signal"], lsb)[1]
              for i in range(n)]
     framed = codecs[name].batch_inference_reads(list_of_reads=small, batch_size=20480)
     for i in range(n):

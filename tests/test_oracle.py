@@ -308,7 +308,7 @@ def test_compress_chunks_matches_reference_e2e(oracle_mod, oracle_models):
         lsb = int(z[f"{name}_lsb"])
         for i in range(int(z[f"{name}_nreads"])):
             sig = z[f"{name}_read{i}_signal"]
-            small = signal.split_signal(signal.prepare_signal(sig, lsb))[1]
+            small = signal.split_signal(sig, lsb)[1]
             chunks = split_into_chunks(small, 2048)
             enc = oracle_mod.compress_chunks(oracle_models[name], chunks)
             framed = frame_chunks(enc)
