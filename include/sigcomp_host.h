@@ -97,6 +97,77 @@ int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *d
                   uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,
                   int64_t *bad);
 
+/* ------------------------------------------------------------ SIG2 records
+ *
+ * A SIG2 archive is MAGIC 'SIG2', a uint32 length and the header blob (the
+ * zstd-compressed pickle of the global metadata, main.py:226-246: opaque
+ * bytes here), then one record per read (main.py:549-607):
+ *   prefix   POD5 source:  REC_FMT '<16sddBBdIIIQ' (62 bytes, sc_pod5_record)
+ *            BLOW5 source: read id (16 bytes), uint32 metadata length,
+ *                          metadata (a pickle: opaque bytes here)
+ *   split header '<hII': sig0 (int16), samples N (uint32), small tokens (uint32)
+ *   three blobs, each a uint32 length then the bytes: the framed range-coded
+ *   small tokens, the Rice-coded large values, the Rice-coded positions.
+ * All integers little-endian, no padding.  The SIDX index (main.py:1451-1502,
+ * archive_shards.py:295-304) is 'SIDX', a uint32 count, then per read the
+ * 16-byte read id and the uint64 file offset of its record. */
+
+#define SC_SIG2_POD5 0
+#define SC_SIG2_BLOW5 1
+#define SC_SIG2_POD5_PREFIX 62
+#define SC_HOST_ERR_TRUNCATED   20  /* record, header or blob cut short [ValueError] */
+#define SC_HOST_ERR_BAD_COUNTS  21  /* N < 1 or small tokens > N - 1 [ValueError] */
+#define SC_HOST_ERR_TRAILING_RECORDS 22  /* bytes after the last record [ValueError] */
+#define SC_HOST_ERR_INDEX       23  /* bad magic / count / size / offset [ValueError] */
+
+/* REC_FMT fields in order (main.py:905-917). */
+typedef struct {
+    uint8_t read_id[16];
+    double calibration_offset, calibration_scale;
+    uint8_t end_reason_forced, end_reason_index;
+    double median_before;
+    uint32_t pore, read_number, run_info;
+    uint64_t start_sample;
+} sc_pod5_record;
+
+/* Serialize n records (_write_read_payload / _write_read_payload_blow5,
+ * main.py:575-597).  Per read r: pod5[r] (POD5) or read_ids[16 r .. +16] and
+ * meta[meta_off[r] .. + meta_len[r]] (BLOW5); sig0[r], n_samples[r],
+ * n_small[r]; the three blobs at blob_off[3 r + k] with blob_len[3 r + k]
+ * bytes in `blobs` (k = 0 small tokens, 1 large values, 2 positions).
+ * Record r is written at out + out_off[r]; its size is prefix + 10 + 12 +
+ * the blob lengths (+ 20 + meta_len for BLOW5 prefixes). */
+int sc_sig2_write_records(int32_t format, int64_t n, const sc_pod5_record *pod5, const uint8_t *read_ids,
+                          const uint8_t *meta, const int64_t *meta_off, const int64_t *meta_len,
+                          const int16_t *sig0, const uint32_t *n_samples, const uint32_t *n_small,
+                          const uint8_t *blobs, const int64_t *blob_off, const int64_t *blob_len, uint8_t *out,
+                          const int64_t *out_off, int32_t n_threads, int64_t *bad);
+
+/* Scan n_reads records from data[start .. size) as scan_archive
+ * (archive_shards.py:149-175) and cmd_index (main.py:1451-1493) do: writes
+ * rec_off[r] (record start; rec_off[n_reads] = end of the last record),
+ * read_ids (16 bytes each), sig0 / n_samples / n_small, the blobs' byte
+ * offsets and lengths (blob_off / blob_len, 3 per read, offsets into data),
+ * meta_off / meta_len (BLOW5; may be NULL for POD5) and pod5 (POD5; may be
+ * NULL).  Fails for a truncated record, N < 1 or more small tokens than
+ * N - 1, a blob past the end of data, or (require_end != 0) bytes left after
+ * the last record. */
+int sc_sig2_scan_records(const uint8_t *data, int64_t size, int64_t start, int64_t n_reads, int32_t format,
+                         int32_t require_end, int64_t *rec_off, uint8_t *read_ids, int16_t *sig0,
+                         uint32_t *n_samples, uint32_t *n_small, int64_t *blob_off, int64_t *blob_len,
+                         int64_t *meta_off, int64_t *meta_len, sc_pod5_record *pod5, int64_t *bad);
+
+/* SIDX index of n reads: 8 + 24 n bytes to out. */
+int sc_sig2_write_index(int64_t n, const uint8_t *read_ids, const uint64_t *offsets, uint8_t *out);
+
+/* Read an SIDX index of `size` bytes for an archive of n_expected reads whose
+ * records span [data_start, file_size) (_checked_index_header and
+ * _index_entry, main.py:427-444): checks the magic, count == n_expected,
+ * size == 8 + 24 count and every offset inside the records; writes read_ids
+ * and offsets.  *bad = the offending entry (-1 for the header). */
+int sc_sig2_read_index(const uint8_t *data, int64_t size, int64_t n_expected, int64_t data_start,
+                       int64_t file_size, uint8_t *read_ids, uint64_t *offsets, int64_t *bad);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,10 @@ const char *err_text(int code) {
         case SC_HOST_ERR_COUNTS: return "small and large value counts disagree with the read length";
         case SC_HOST_ERR_POSITION: return "large-value position outside the read";
         case SC_HOST_ERR_EMPTY_READ: return "a read has no samples";
+        case SC_HOST_ERR_TRUNCATED: return "Truncated SIG2 read record";
+        case SC_HOST_ERR_BAD_COUNTS: return "Invalid sample or token count in SIG2 read record";
+        case SC_HOST_ERR_TRAILING_RECORDS: return "SIG2 read count disagrees with trailing file data";
+        case SC_HOST_ERR_INDEX: return "Index count/size does not match the archive; rebuild the index";
         default: return "error";
     }
 }
@@ -286,6 +290,227 @@ int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *d
         if (pos != size) fb.report(r, SC_HOST_ERR_TRAILING);
     });
     return finish(fb, bad);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- SIG2 records
+
+namespace {
+
+template <class T>
+inline void put(uint8_t *&o, T v) {
+    std::memcpy(o, &v, sizeof(T));   // little-endian host
+    o += sizeof(T);
+}
+
+template <class T>
+inline T get(const uint8_t *p) {
+    T v;
+    std::memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+constexpr int64_t SPLIT_HDR = 10;   // '<hII'
+
+}  // namespace
+
+extern "C" {
+
+int sc_sig2_write_records(int32_t format, int64_t n, const sc_pod5_record *pod5, const uint8_t *read_ids,
+                          const uint8_t *meta, const int64_t *meta_off, const int64_t *meta_len,
+                          const int16_t *sig0, const uint32_t *n_samples, const uint32_t *n_small,
+                          const uint8_t *blobs, const int64_t *blob_off, const int64_t *blob_len, uint8_t *out,
+                          const int64_t *out_off, int32_t n_threads, int64_t *bad) {
+    const bool blow5 = format == SC_SIG2_BLOW5;
+    if (n < 0 || (format != SC_SIG2_POD5 && !blow5) ||
+        (n && (!sig0 || !n_samples || !n_small || !blobs || !blob_off || !blob_len || !out || !out_off ||
+               (blow5 ? (!read_ids || !meta || !meta_off || !meta_len) : !pod5)))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n, n_threads, [&](int64_t r) {
+        if (n_samples[r] < 1 || n_small[r] > n_samples[r] - 1) {
+            fb.report(r, SC_HOST_ERR_BAD_COUNTS);
+            return;
+        }
+        for (int k = 0; k < 3; ++k)
+            if (blob_len[3 * r + k] < 0 || blob_len[3 * r + k] > 0xFFFFFFFFll) {
+                fb.report(r, SC_HOST_ERR_OVERSIZE);
+                return;
+            }
+        if (blow5 && (meta_len[r] < 0 || meta_len[r] > 0xFFFFFFFFll)) {
+            fb.report(r, SC_HOST_ERR_OVERSIZE);
+            return;
+        }
+        uint8_t *o = out + out_off[r];
+        if (blow5) {
+            std::memcpy(o, read_ids + 16 * r, 16);
+            o += 16;
+            put<uint32_t>(o, (uint32_t)meta_len[r]);
+            std::memcpy(o, meta + meta_off[r], (size_t)meta_len[r]);
+            o += meta_len[r];
+        } else {
+            const sc_pod5_record &p = pod5[r];
+            std::memcpy(o, p.read_id, 16);
+            o += 16;
+            put<double>(o, p.calibration_offset);
+            put<double>(o, p.calibration_scale);
+            put<uint8_t>(o, p.end_reason_forced);
+            put<uint8_t>(o, p.end_reason_index);
+            put<double>(o, p.median_before);
+            put<uint32_t>(o, p.pore);
+            put<uint32_t>(o, p.read_number);
+            put<uint32_t>(o, p.run_info);
+            put<uint64_t>(o, p.start_sample);
+        }
+        put<int16_t>(o, sig0[r]);
+        put<uint32_t>(o, n_samples[r]);
+        put<uint32_t>(o, n_small[r]);
+        for (int k = 0; k < 3; ++k) {
+            const int64_t len = blob_len[3 * r + k];
+            put<uint32_t>(o, (uint32_t)len);
+            std::memcpy(o, blobs + blob_off[3 * r + k], (size_t)len);
+            o += len;
+        }
+    });
+    return finish(fb, bad);
+}
+
+int sc_sig2_scan_records(const uint8_t *data, int64_t size, int64_t start, int64_t n_reads, int32_t format,
+                         int32_t require_end, int64_t *rec_off, uint8_t *read_ids, int16_t *sig0,
+                         uint32_t *n_samples, uint32_t *n_small, int64_t *blob_off, int64_t *blob_len,
+                         int64_t *meta_off, int64_t *meta_len, sc_pod5_record *pod5, int64_t *bad) {
+    const bool blow5 = format == SC_SIG2_BLOW5;
+    if (n_reads < 0 || size < 0 || start < 0 || start > size || (format != SC_SIG2_POD5 && !blow5) ||
+        !rec_off || (n_reads && (!data || !read_ids || !sig0 || !n_samples || !n_small || !blob_off ||
+                                 !blob_len || (blow5 && (!meta_off || !meta_len))))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    int64_t pos = start;
+    for (int64_t r = 0; r < n_reads; ++r) {
+        rec_off[r] = pos;
+        if (blow5) {
+            if (pos + 20 > size) {
+                fb.report(r, SC_HOST_ERR_TRUNCATED);
+                break;
+            }
+            std::memcpy(read_ids + 16 * r, data + pos, 16);
+            const int64_t ml = get<uint32_t>(data + pos + 16);
+            pos += 20;
+            if (pos + ml > size) {
+                fb.report(r, SC_HOST_ERR_TRUNCATED);
+                break;
+            }
+            meta_off[r] = pos;
+            meta_len[r] = ml;
+            pos += ml;
+        } else {
+            if (pos + SC_SIG2_POD5_PREFIX > size) {
+                fb.report(r, SC_HOST_ERR_TRUNCATED);
+                break;
+            }
+            const uint8_t *p = data + pos;
+            std::memcpy(read_ids + 16 * r, p, 16);
+            if (pod5) {
+                sc_pod5_record &q = pod5[r];
+                std::memcpy(q.read_id, p, 16);
+                q.calibration_offset = get<double>(p + 16);
+                q.calibration_scale = get<double>(p + 24);
+                q.end_reason_forced = p[32];
+                q.end_reason_index = p[33];
+                q.median_before = get<double>(p + 34);
+                q.pore = get<uint32_t>(p + 42);
+                q.read_number = get<uint32_t>(p + 46);
+                q.run_info = get<uint32_t>(p + 50);
+                q.start_sample = get<uint64_t>(p + 54);
+            }
+            pos += SC_SIG2_POD5_PREFIX;
+        }
+        if (pos + SPLIT_HDR > size) {
+            fb.report(r, SC_HOST_ERR_TRUNCATED);
+            break;
+        }
+        sig0[r] = get<int16_t>(data + pos);
+        n_samples[r] = get<uint32_t>(data + pos + 2);
+        n_small[r] = get<uint32_t>(data + pos + 6);
+        pos += SPLIT_HDR;
+        if (n_samples[r] < 1 || n_small[r] > n_samples[r] - 1) {
+            fb.report(r, SC_HOST_ERR_BAD_COUNTS);
+            break;
+        }
+        bool ok = true;
+        for (int k = 0; k < 3 && ok; ++k) {
+            if (pos + 4 > size) {
+                ok = false;
+                break;
+            }
+            const int64_t len = get<uint32_t>(data + pos);
+            pos += 4;
+            if (pos + len > size) {
+                ok = false;
+                break;
+            }
+            blob_off[3 * r + k] = pos;
+            blob_len[3 * r + k] = len;
+            pos += len;
+        }
+        if (!ok) {
+            fb.report(r, SC_HOST_ERR_TRUNCATED);
+            break;
+        }
+    }
+    if (fb.idx == INT64_MAX) {
+        rec_off[n_reads] = pos;
+        if (require_end && pos != size) fb.report(n_reads, SC_HOST_ERR_TRAILING_RECORDS);
+    }
+    return finish(fb, bad);
+}
+
+int sc_sig2_write_index(int64_t n, const uint8_t *read_ids, const uint64_t *offsets, uint8_t *out) {
+    if (n < 0 || n > 0xFFFFFFFFll || !out || (n && (!read_ids || !offsets))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    uint8_t *o = out;
+    std::memcpy(o, "SIDX", 4);
+    o += 4;
+    put<uint32_t>(o, (uint32_t)n);
+    for (int64_t r = 0; r < n; ++r) {
+        std::memcpy(o, read_ids + 16 * r, 16);
+        o += 16;
+        put<uint64_t>(o, offsets[r]);
+    }
+    return SC_OK;
+}
+
+int sc_sig2_read_index(const uint8_t *data, int64_t size, int64_t n_expected, int64_t data_start,
+                       int64_t file_size, uint8_t *read_ids, uint64_t *offsets, int64_t *bad) {
+    if (size < 0 || n_expected < 0 || (size && !data) || (n_expected && (!read_ids || !offsets))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    auto fail_at = [&](int64_t i, const char *msg) {
+        if (bad) *bad = i;
+        g_err = msg;
+        return SC_HOST_ERR_INDEX;
+    };
+    if (size < 8 || std::memcmp(data, "SIDX", 4) != 0) return fail_at(-1, "Not a valid SIDX index");
+    const int64_t count = get<uint32_t>(data + 4);
+    if (count != n_expected || size != 8 + 24 * count)
+        return fail_at(-1, "Index count/size does not match the archive; rebuild the index");
+    for (int64_t r = 0; r < count; ++r) {
+        const uint8_t *e = data + 8 + 24 * r;
+        const uint64_t off = get<uint64_t>(e + 16);
+        if (!((uint64_t)data_start <= off && off < (uint64_t)file_size))
+            return fail_at(r, "SIDX entry points outside archive records; rebuild the index");
+        std::memcpy(read_ids + 16 * r, e, 16);
+        offsets[r] = off;
+    }
+    return SC_OK;
 }
 
 }  // extern "C"
