@@ -623,6 +623,30 @@ std::vector<int8_t> pack_weight(const int8_t *w, int n, int k, bool perm_k) {
 
 hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
+// Per-step cost of a full-wave decode launch at rt = 1 .. DEC_RT_MAX row
+// tiles per workgroup (MI355X, 512-token chunks, lossless model; us x 10 per
+// step; rt <= 4 runs the pipelined core).  Per row tile rt = 3 is cheapest
+// (41.4 us), rt = 1 the dearest (64.4 us).
+constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 644, 888, 1241, 1680, 2211, 2622};
+
+// Split `units` row tiles per CU into launch sizes of least summed step cost
+// (largest first, so that they take the longest chunks).
+std::vector<int> dec_plan(int64_t units) {
+    std::vector<int64_t> best((size_t)units + 1, INT64_MAX);
+    std::vector<int> pick((size_t)units + 1, 0);
+    best[0] = 0;
+    for (int64_t u = 1; u <= units; ++u)
+        for (int rt = 1; rt <= DEC_RT_MAX && rt <= u; ++rt)
+            if (best[u - rt] + DEC_STEP_COST[rt] < best[u]) {
+                best[u] = best[u - rt] + DEC_STEP_COST[rt];
+                pick[u] = rt;
+            }
+    std::vector<int> plan;
+    for (int64_t u = units; u > 0; u -= pick[u]) plan.push_back(pick[u]);
+    std::sort(plan.rbegin(), plan.rend());
+    return plan;
+}
+
 template <int RT>
 void dec_launch(const sc_model *m, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                 const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
@@ -895,19 +919,32 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     DeviceGuard guard(m->device);
     hipStream_t s = as_stream(stream);
     // Launch plan.  A workgroup owns 32*rt consecutive chunks for the whole
-    // decode, one workgroup per CU.  Each launch is one full wave of n_cu
-    // workgroups at the largest rt that fills it (rt <= DEC_RT_MAX); the
-    // chunks left over (fewer than 32*n_cu) go to a final launch of rt = 1
-    // workgroups.  With chunks sorted longest first, the leftover launch
-    // holds the shortest chunks and ends quickly.
+    // decode, one workgroup per CU, and every launch but the last is one
+    // full wave of n_cu workgroups.  The chunks of the full waves make
+    // `units` row tiles per CU; with the pipelined core they are split into
+    // launches by dec_plan (measured step costs), otherwise taken greedily
+    // at the largest rt.  The chunks left over (fewer than 32*n_cu) go to a
+    // final launch of rt = 1 workgroups.  With chunks sorted longest first
+    // the largest tiles get the longest chunks and the leftover launch the
+    // shortest ones.
     const int64_t cu = m->n_cu;
+    const int64_t units = n_chunks / (32 * cu);
+    std::vector<int> plan;
+    const char *plan_env = getenv("SC_HIP_DEC_PLAN");   // "greedy": largest rt first (comparisons)
+    if (m->dev.pipe && !(plan_env && std::strcmp(plan_env, "greedy") == 0)) {
+        plan = dec_plan(units);
+    } else {
+        for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, DEC_RT_MAX))
+            plan.push_back((int)std::min<int64_t>(u, DEC_RT_MAX));
+    }
     int64_t start = 0;
+    size_t step = 0;
     while (start < n_chunks) {
         const int64_t left = n_chunks - start;
-        int64_t rt = std::min<int64_t>(left / (32 * cu), DEC_RT_MAX);
-        int64_t count;
+        int64_t rt, count;
         unsigned grid;
-        if (rt >= 1) {
+        if (step < plan.size()) {
+            rt = plan[step++];
             count = cu * 32 * rt;
             grid = (unsigned)cu;
         } else {
