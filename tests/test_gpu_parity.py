@@ -233,3 +233,24 @@ def test_plain_core_matches_oracle(oracle_mod, monkeypatch, which):
 
 def test_pipelined_core_selected_for_bundled_models(codecs):
     assert codecs["lossless"].hip.pipelined and codecs["lossy"].hip.pipelined
+
+
+@pytest.mark.parametrize("units,extra", [(2, 7), (3, 0), (4, 31), (5, 1), (6, 500)])
+def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, units, extra):
+    """Chunk counts that fill `units` full waves of 32-chunk row tiles per CU
+    (split by the launch planner into 64/96/128-chunk workgroup launches)
+    plus a partial leftover launch; short random chunk lengths."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    n = units * 32 * n_cu + extra
+    rng = np.random.default_rng(units * 1000 + extra)
+    lengths = rng.integers(1, 40, n).astype(np.int32)
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    back, tok_off = codec.decompress_flat(words, woff, wcnt, lengths)
+    assert np.array_equal(back, tokens)
+    sample = rng.choice(n, 16, replace=False)
+    off = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    chunks = [tokens[off[i]:off[i] + lengths[i]] for i in sample]
+    ref = oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    assert [words[woff[i]:woff[i] + wcnt[i]].tobytes() for i in sample] == ref
