@@ -82,9 +82,11 @@ __device__ __forceinline__ void load_emb_lds(const int8_t *__restrict__ emb, uin
     }
 }
 
-// The exp-LUT is staged in LDS as float64 (entries <= 2**38 are exact).
-__device__ __forceinline__ void load_lut_lds(const uint64_t *__restrict__ lut, double *s_lut) {
-    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_lut[i] = (double)lut[i];
+// The exp-LUT is staged in LDS reversed, s_rlut[j] = LUT[255 - j], as
+// float64 (entries <= 2**38 are exact): LUT[max - l] = s_rlut[255 - max + l]
+// is then one shift-add from the signed logit l (see row_freq).
+__device__ __forceinline__ void load_lut_lds(const uint64_t *__restrict__ lut, double *s_rlut) {
+    for (int i = threadIdx.x; i < VOCAB; i += blockDim.x) s_rlut[VOCAB - 1 - i] = (double)lut[i];
 }
 
 // ---------------------------------------------------------------- wave primitives
@@ -581,24 +583,54 @@ __device__ __forceinline__ double row16_sum_f64(double x) {
     return x + dpp_f64<DPP_MIRROR>(x);
 }
 
-// cpu_entropy_coding.py:90-110: u = LUT[max - l]; T = sum u;
-// f = max(u*2**24 // T, 1); the first argmax absorbs sum(f) - 2**24.
+// cpu_entropy_coding.py:90-110: w = LUT[max - l]; T = sum w;
+// f = max(w*2**24 // T, 1); the first argmax absorbs sum(f) - 2**24.
 //
-// s_lut holds the LUT as float64 (every entry <= 2**38 is exact), so u and
-// every partial sum of T (integers < 2**53) are exact.  q = u * (2**24 / T)
-// is within 2**-28 of the true quotient (two roundings of relative 2**-53,
-// quotients <= 2**24), so floor(q) is exact unless q lies within 2**-20 of
-// an integer; a row with such a value redoes its 16 quotients with the
-// exact integer division (div_floor_est).
+// Exactness.  w and every partial sum of T are integers below 2**53, exact
+// in float64 (s_rlut is the reversed LUT, see load_lut_lds).  r24 = 2**24/T
+// is the hardware reciprocal refined by two Newton-Raphson steps
+// (r += r (1 - T r)), relative error below 2**-50, and qe = w r24 + 2**-20
+// (one fma) lies within 2**-26 of Q + 2**-20, Q = w 2**24 / T the exact
+// quotient.  So floor(qe) = floor(Q) unless Q lies less than 2**-20 + 2**-26
+// below an integer, which needs fract(qe) < 2**-19.  Below 2 either floor
+// gives f = max(., 1) = 1, so qe is clamped to >= 1.5 first and only
+// quotients >= 2 are checked (w = 0, the LUT's zero tail, never is).  A lane
+// with a flagged quotient redoes its 16 with exact integer division
+// (div_floor_est).
 //
-// N rows at once (N independent 16-lane rows per lane group): the phases
-// of the N rows are interleaved in straight-line code so their latency
-// chains (LDS lookups, DPP reductions, float64 division) overlap; only the
-// rare exact-division fallback is a branch, taken when any of the N rows
-// needs it.
+// The argmax correction stays per-lane data instead of a per-symbol update:
+// the row's first argmax is the row maximum of the key
+// (f - 1) << 8 | (15 - u) << 4 | (15 - k) (higher f first, then the lower
+// symbol index 16u + k; f <= 2**24 so the key fits 32 bits), and only the
+// lane that holds it gets kfix < 16.
+struct RowFreq {
+    uint32_t f[16];   // symbols 16u .. 16u+15 before the argmax correction
+    uint32_t ex;      // corrected exclusive cumulative frequency of symbol 16u
+    uint32_t tot;     // corrected sum of this lane's 16 frequencies
+    uint32_t kfix;    // k of the row's first argmax if this lane holds it, else 16
+    uint32_t ffix;    // corrected frequency of the first argmax
+};
+
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t x) {
+    x = max(x, (uint32_t)dpp<DPP_XOR1>((int)x));
+    x = max(x, (uint32_t)dpp<DPP_XOR2>((int)x));
+    x = max(x, (uint32_t)dpp<DPP_HALF_MIRROR>((int)x));
+    return max(x, (uint32_t)dpp<DPP_MIRROR>((int)x));
+}
+
+// reciprocal of a float64 in [1, 2**64): the hardware estimate refined by
+// two Newton-Raphson steps
+__device__ __forceinline__ double recip_nr(double x) {
+    double r = __builtin_amdgcn_rcp(x);
+    r = __builtin_fma(r, __builtin_fma(-x, r, 1.0), r);
+    return __builtin_fma(r, __builtin_fma(-x, r, 1.0), r);
+}
+
+// N rows at once (N independent 16-lane rows per lane group): the phases of
+// the N rows are interleaved in straight-line code so that their latency
+// chains (LDS lookups, DPP reductions, float64 arithmetic) overlap.
 template <int N>
-__device__ __forceinline__ void row_frequencies16n(const v4i (&raw)[N], const double *s_lut, int u,
-                                                   Freq16 (&o)[N]) {
+__device__ __forceinline__ void row_freq(const v4i (&raw)[N], const double *s_rlut, int u, RowFreq (&o)[N]) {
     int l[N][16];
     int m[N];
 #pragma unroll
@@ -612,95 +644,142 @@ __device__ __forceinline__ void row_frequencies16n(const v4i (&raw)[N], const do
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) m[n] = row16_max(m[n]);
-    double uu[N][16];
+    double w[N][16];
     double T[N];
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-        double tl = 0.0;
+        const double *p = s_rlut + (VOCAB - 1 - m[n]);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            uu[n][k] = s_lut[m[n] - l[n][k]];
-            tl += uu[n][k];
-        }
-        T[n] = tl;
+        for (int k = 0; k < 16; ++k) w[n][k] = p[l[n][k]];
+        double s[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s[k] = w[n][2 * k] + w[n][2 * k + 1];
+        T[n] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) T[n] = row16_sum_f64(T[n]);
-    bool near = false;
+    double r24[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) r24[n] = recip_nr(T[n]) * 16777216.0;
+    uint32_t hmin = 0xFFFFFFFFu;
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-        const double r24 = 16777216.0 / T[n];
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const double q = uu[n][k] * r24;
-            const double fr = q - __builtin_floor(q);
-            near = near || fr < 0x1p-20 || fr > 1.0 - 0x1p-20;
-            const uint32_t fq = (uint32_t)q;
-            o[n].f[k] = fq < 1u ? 1u : fq;
+            const double qe = __builtin_fmax(__builtin_fma(w[n][k], r24[n], 0x1p-20), 1.5);
+            o[n].f[k] = (uint32_t)qe;
+            hmin = min(hmin, (uint32_t)(__builtin_bit_cast(uint64_t, __builtin_amdgcn_fract(qe)) >> 32));
         }
     }
-    if (near) {
+    // high word of 2**-19: a non-negative double is below 2**-19 iff its
+    // high word is below this
+    if (hmin < 0x3EC00000u) {
 #pragma unroll
         for (int n = 0; n < N; ++n) {
             const uint64_t Ti = (uint64_t)T[n];
-            const double rT = 1.0 / T[n];
+            const double rT = r24[n] * 0x1p-24;
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const uint64_t q = div_floor_est(((uint64_t)uu[n][k]) << 24, Ti, rT);
+                const uint64_t q = div_floor_est(((uint64_t)w[n][k]) << 24, Ti, rT);
                 o[n].f[k] = q < 1 ? 1u : (uint32_t)q;
             }
         }
     }
-    uint32_t S[N];
-    int fm[N];
+    const uint32_t lanebits = (uint32_t)(15 - u) << 4;
+    uint32_t S[N], K[N];
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-        uint32_t sl = 0, fl = 0;
+        uint32_t sl = 0, km = 0;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             sl += o[n].f[k];
-            fl = max(fl, o[n].f[k]);
+            km = max(km, (o[n].f[k] << 4) | (uint32_t)(15 - k));
         }
+        o[n].tot = sl;
         S[n] = sl;
-        fm[n] = (int)fl;
+        K[n] = (((km << 4) - 256u) & 0xFFFFFF00u) | lanebits | (km & 15u);
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) {
         S[n] = row16_sum(S[n]);
-        fm[n] = row16_max(fm[n]);
+        K[n] = row16_max_u32(K[n]);
     }
-    int idx[N];
 #pragma unroll
     for (int n = 0; n < N; ++n) {
-        int cand = 1 << 20;
-#pragma unroll
-        for (int k = 15; k >= 0; --k)
-            if ((int)o[n].f[k] == fm[n]) cand = 16 * u + k;
-        idx[n] = cand;
+        const uint32_t adj = S[n] - TOTAL;   // sum(f) - 2**24, mod 2**32
+        const bool star = (K[n] & 0xF0u) == lanebits;
+        o[n].ffix = (K[n] >> 8) + 1u - adj;
+        o[n].kfix = star ? 15u - (K[n] & 15u) : 16u;
+        if (star) o[n].tot -= adj;
     }
 #pragma unroll
-    for (int n = 0; n < N; ++n) idx[n] = row16_min(idx[n]);
-    uint32_t tot[N];
-#pragma unroll
-    for (int n = 0; n < N; ++n) {
-        const bool mine = (idx[n] >> 4) == u;
-#pragma unroll
-        for (int k = 0; k < 16; ++k)
-            if (mine && (idx[n] & 15) == k) o[n].f[k] -= S[n] - TOTAL;
-        uint32_t t = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) t += o[n].f[k];
-        tot[n] = t;
-    }
-#pragma unroll
-    for (int n = 0; n < N; ++n) o[n].ex = row16_excl_scan(tot[n]);
+    for (int n = 0; n < N; ++n) o[n].ex = row16_excl_scan(o[n].tot);
 }
 
-__device__ __forceinline__ void row_frequencies16(v4i raw, const double *s_lut, int u, Freq16 &o) {
+// corrected frequency of symbol 16u + k
+__device__ __forceinline__ uint32_t row_freq_at(const RowFreq &o, int k) {
+    return (uint32_t)k == o.kfix ? o.ffix : o.f[k];
+}
+
+// The whole corrected table, lane u's 16 entries (full-CDF and step paths).
+template <int N>
+__device__ __forceinline__ void row_frequencies16n(const v4i (&raw)[N], const double *s_rlut, int u,
+                                                   Freq16 (&o)[N]) {
+    RowFreq rf[N];
+    row_freq<N>(raw, s_rlut, u, rf);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) o[n].f[k] = row_freq_at(rf[n], k);
+        o[n].ex = rf[n].ex;
+    }
+}
+
+__device__ __forceinline__ void row_frequencies16(v4i raw, const double *s_rlut, int u, Freq16 &o) {
     const v4i r[1] = {raw};
     Freq16 f[1];
-    row_frequencies16n<1>(r, s_lut, u, f);
+    row_frequencies16n<1>(r, s_rlut, u, f);
     o = f[0];
+}
+
+// ---- symbol lookups through a per-row LDS slot --------------------------
+//
+// A row's 16 lanes hold 16 symbols each.  To find the cumulative frequency
+// of a given symbol (encoder) or the symbol whose interval holds a quantile
+// (decoder) without a 16-step select chain in every lane, the lane whose
+// segment holds it (the owner) writes its 16 frequencies and
+// {ex, kfix, ffix, owner} to the row's slot; lane j of the row then reads
+// frequency j of that segment, applies the argmax correction and a 16-lane
+// prefix sum gives each lane its symbol's cumulative frequency.  The owner's
+// write and the row's reads are in one wavefront: LDS executes a
+// wavefront's accesses in order, slot_sync only keeps the compiler from
+// moving them.
+constexpr int SLOT_DWORDS = 20;
+
+__device__ __forceinline__ void slot_put(uint32_t *slot, const RowFreq &o, int u) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    v4u *s = (v4u *)slot;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = v4u{o.f[4 * j], o.f[4 * j + 1], o.f[4 * j + 2], o.f[4 * j + 3]};
+    s[4] = v4u{o.ex, o.kfix, o.ffix, (uint32_t)u};
+}
+
+__device__ __forceinline__ void slot_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// lane u's symbol of the slot's segment: its cumulative frequency and
+// frequency; returns the owner lane (the symbol is 16 * owner + u)
+__device__ __forceinline__ uint32_t slot_get(const uint32_t *slot, int u, uint32_t &cum, uint32_t &freq) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u meta = *(const v4u *)(slot + 16);
+    uint32_t f = slot[u];
+    if ((uint32_t)u == meta[1]) f = meta[2];
+    cum = meta[0] + row16_excl_scan(f);
+    freq = f;
+    return meta[3];
 }
 
 // cumulative frequency and frequency of local symbol k (0..15) of this lane
@@ -794,19 +873,27 @@ __device__ __forceinline__ int enc_seal(EncState &s, uint32_t *__restrict__ out,
     return 0;
 }
 
-// Decoder quantile (point - lower) // scale, exact for quotients below
-// 2**24; false when the quotient is >= 2**24 (an invalid stream,
-// cpu_entropy_coding.py:240-248).  q0 is clamped to 2**24 before the
-// product so that q0*scale <= 2**24*scale <= range never wraps.
+// a * b for a < 2**40, b < 2**24 (a coder scale times a frequency or a
+// cumulative frequency): the high word of a times b fits the 24-bit multiply
+__device__ __forceinline__ uint64_t mul_scale(uint64_t a, uint32_t b) {
+    return (uint64_t)(uint32_t)a * b + ((uint64_t)__umul24((uint32_t)(a >> 32), b) << 32);
+}
+
+// Decoder quantile (point - lower) // scale for 0 < scale < 2**40 (range >>
+// 24), exact for quotients below 2**24; false when the quotient is >= 2**24
+// (an invalid stream, cpu_entropy_coding.py:240-248).  The float64 estimate
+// D * (1/scale) (D rounded once, the reciprocal within 2**-50) is within one
+// of the quotient; it is clamped to 2**24 - 1 so that q0 * scale never wraps,
+// and one integer step corrects it (a quotient >= 2**24 ends at 2**24).
 __device__ __forceinline__ bool dec_quantile(uint64_t D, uint64_t scale, uint32_t &q) {
-    const double qe = (double)D * (1.0 / (double)scale);
-    uint64_t q0 = qe >= 16777216.0 ? 16777216ull : (uint64_t)qe;
-    const uint64_t prod = q0 * scale;
+    const double Df = __builtin_fma((double)(uint32_t)(D >> 32), 0x1p32, (double)(uint32_t)D);
+    const double sf = __builtin_fma((double)(uint32_t)(scale >> 32), 0x1p32, (double)(uint32_t)scale);
+    uint32_t q0 = (uint32_t)__builtin_fmin(Df * recip_nr(sf), 16777215.0);
+    const uint64_t prod = mul_scale(scale, q0);
     if (prod > D) q0 -= 1;
     else if (D - prod >= scale) q0 += 1;
-    if (q0 >= TOTAL) return false;
-    q = (uint32_t)q0;
-    return true;
+    q = q0;
+    return q0 < TOTAL;
 }
 
 // Symbol search on a 16-lane row: largest v with excl_cdf[v] <= q (the

@@ -155,9 +155,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                                                              const int32_t *__restrict__ lengths,
                                                              int64_t n_chunks, const int32_t *__restrict__ tile_start,
                                                              uint2 *__restrict__ pairs) {
+    constexpr int EPI_N = 2;   // row groups per epilogue iteration; R_TILE / 4 is a multiple of EPI_N * WAVES
+    static_assert((R_TILE / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must stay inside the tile");
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ double s_lut[VOCAB];
     __shared__ int64_t s_chunk;
@@ -193,22 +196,31 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
         mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
                                 wave, lane);
         const int32_t valid = min(R_TILE, L - t0);
-        // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n
-        for (int gi = wave; gi * 4 < valid; gi += 2 * WAVES) {
-            const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
-            const v4i raw[2] = {*(const v4i *)(s_act + act_at<PIPE>(rr[0], u)),
-                                *(const v4i *)(s_act + act_at<PIPE>(rr[1], u))};
-            Freq16 fr[2];
-            row_frequencies16n<2>(raw, s_lut, u, fr);
+        // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.  The
+        // lane holding the row's token publishes its 16 symbols in the row's
+        // slot; the lane whose index is the token's low 4 bits stores its
+        // (cumulative frequency, frequency) pair.
+        uint32_t *slots = s_slot + wave * (EPI_N * 4 * SLOT_DWORDS);
+        for (int gi = wave; gi * 4 < valid; gi += EPI_N * WAVES) {
+            int rr[EPI_N], sym[EPI_N];
+            v4i raw[EPI_N];
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                const int r = rr[n];
-                const int s = s_tok[r + WIN];
-                if (r < valid && (s >> 4) == u) {
-                    uint32_t cum, freq;
-                    freq16_at(fr[n], s & 15, cum, freq);
-                    out[t0 + r] = make_uint2(cum, freq);
-                }
+            for (int n = 0; n < EPI_N; ++n) {
+                rr[n] = (gi + n * WAVES) * 4 + q4;
+                sym[n] = s_tok[rr[n] + WIN];
+                raw[n] = *(const v4i *)(s_act + act_at<PIPE>(rr[n], u));
+            }
+            RowFreq fr[EPI_N];
+            row_freq<EPI_N>(raw, s_lut, u, fr);
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n)
+                if ((sym[n] >> 4) == u) slot_put(slots + (n * 4 + q4) * SLOT_DWORDS, fr[n], u);
+            slot_sync();
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                uint32_t cum, freq;
+                slot_get(slots + (n * 4 + q4) * SLOT_DWORDS, u, cum, freq);
+                if (rr[n] < valid && (sym[n] & 15) == u) out[t0 + rr[n]] = make_uint2(cum, freq);
             }
         }
     }
@@ -258,9 +270,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                                            const int64_t *__restrict__ tok_off,
                                                            int32_t *__restrict__ status) {
     constexpr int R = 32 * RT;
+    constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
+    static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
+    __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
@@ -308,21 +323,26 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
                            },
                            wave, lane);
-        // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n.
-        // _decode_partition (cpu_entropy_coding.py:230-266): the 16 lanes of a
-        // row compute the same state, lane u == 0 stores it.  The word a
-        // renormalisation would shift in is loaded before the frequency work
-        // (whether or not this step needs it) so its latency is hidden.
-        for (int gi = wave; gi < R / 4; gi += 2 * WAVES) {
-            const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
-            uint64_t lower[2], range[2], point[2];
-            int32_t rpos[2];
-            uint32_t wnext[2];
-            bool active[2];
-            v4i raw[2];
+        // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
+        // _decode_partition (cpu_entropy_coding.py:230-266): every lane of a
+        // row computes the row's quantile; the lane whose 16 symbols hold it
+        // publishes them in the row's slot and the lane that finds the
+        // symbol there (its interval holds the quantile) stores the new
+        // state.  The word a renormalisation would shift in is loaded before
+        // the frequency work (whether or not this step needs it) so its
+        // latency is hidden.
+        uint32_t *slots = s_slot + wave * (EPI_N * 4 * SLOT_DWORDS);
+        for (int gi = wave; gi < R / 4; gi += EPI_N * WAVES) {
+            int rr[EPI_N];
+            uint64_t lower[EPI_N], range[EPI_N], point[EPI_N];
+            int32_t rpos[EPI_N];
+            uint32_t wnext[EPI_N];
+            bool active[EPI_N];
+            v4i raw[EPI_N];
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                const int r = rr[n];
+            for (int n = 0; n < EPI_N; ++n) {
+                const int r = (gi + n * WAVES) * 4 + q4;
+                rr[n] = r;
                 active[n] = t < s_len[r] && s_stat[r] == 0;
                 lower[n] = s_lower[r];
                 range[n] = s_range[r];
@@ -331,35 +351,40 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                 wnext[n] = rpos[n] < s_wcnt[r] ? words[s_woff[r] + rpos[n]] : 0u;
                 raw[n] = *(const v4i *)(s_act + act_at<PIPE>(r, u));
             }
-            Freq16 fr[2];
-            row_frequencies16n<2>(raw, s_lut, u, fr);
+            RowFreq fr[EPI_N];
+            row_freq<EPI_N>(raw, s_lut, u, fr);
+            uint32_t q[EPI_N];
+            bool ok[EPI_N];
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
-                const int r = rr[n];
+            for (int n = 0; n < EPI_N; ++n) {
                 const uint64_t scale = range[n] >> 24;
-                uint32_t q = 0;
-                const bool ok = scale != 0 && dec_quantile(point[n] - lower[n], scale, q);
+                q[n] = 0;
+                ok[n] = scale != 0 && dec_quantile(point[n] - lower[n], scale, q[n]);
+                if (ok[n] && q[n] - fr[n].ex < fr[n].tot) slot_put(slots + (n * 4 + q4) * SLOT_DWORDS, fr[n], u);
+            }
+            slot_sync();
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                const int r = rr[n];
                 uint32_t cum, freq;
-                const int sym = dec_symbol16(fr[n], q, lane, cum, freq);
-                if (active[n] && u == 0) {
-                    if (!ok) {
-                        s_stat[r] = SC_STATUS_INVALID_STREAM;
-                    } else {
-                        uint64_t lo = lower[n] + scale * cum, ra = scale * freq, pt = point[n];
-                        int32_t rp = rpos[n];
-                        if (ra < (1ull << 32)) {
-                            lo <<= 32;
-                            ra <<= 32;
-                            pt = (pt << 32) | wnext[n];
-                            rp += 1;
-                        }
-                        s_lower[r] = lo;
-                        s_range[r] = ra;
-                        s_point[r] = pt;
-                        s_rpos[r] = rp;
-                        s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
+                const uint32_t owner = slot_get(slots + (n * 4 + q4) * SLOT_DWORDS, u, cum, freq);
+                if (active[n] && ok[n] && q[n] - cum < freq) {
+                    const uint64_t scale = range[n] >> 24;
+                    uint64_t lo = lower[n] + mul_scale(scale, cum), ra = mul_scale(scale, freq), pt = point[n];
+                    int32_t rp = rpos[n];
+                    if (ra < (1ull << 32)) {
+                        lo <<= 32;
+                        ra <<= 32;
+                        pt = (pt << 32) | wnext[n];
+                        rp += 1;
                     }
+                    s_lower[r] = lo;
+                    s_range[r] = ra;
+                    s_point[r] = pt;
+                    s_rpos[r] = rp;
+                    s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)(owner * 16 + u);
                 }
+                if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
             }
         }
         __syncthreads();

@@ -76,6 +76,40 @@ def test_int8_logits_to_cdf_matches_reference(int_models, name):
     assert np.array_equal(got.cpu().numpy(), c["cdf"])
 
 
+def _adversarial_logits(rng):
+    """Rows aimed at the frequency rule's corner cases: constant rows (every
+    quotient an exact integer, the exact-division path), argmax ties inside
+    one lane's 16 symbols and across lanes (first argmax wins), one-hot rows
+    (with the lossy LUT's zero tail one frequency is 2**24 before the
+    correction), two-level rows, narrow and wide random rows."""
+    rows = [np.full(256, v) for v in (-128, -1, 0, 1, 127)]
+    for pos in [(0,), (15,), (16,), (255,), (16, 17), (255, 16, 17), (31, 30), (240, 15), (3, 200)]:
+        for hi, lo in ((127, -128), (5, 0), (-60, -128)):
+            r = np.full(256, lo)
+            r[list(pos)] = hi
+            rows.append(r)
+    idx = np.arange(256)
+    for a, b in [(0, 1), (0, -1), (10, -10), (127, -128), (3, 2), (-128, 127)]:
+        rows += [np.where(idx % 2 == 0, a, b), np.where(idx < 128, a, b), np.where(idx % 16 == 0, a, b),
+                 np.where(idx % 16 == 15, a, b)]
+    for spread in (1, 2, 4, 8, 32, 128):
+        rows += list(rng.integers(-spread, spread + 1, (300, 256)) + rng.integers(-100, 100, (300, 1)))
+    rows += list(rng.integers(-128, 128, (3000, 256)))
+    return np.clip(np.array(rows), -128, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_logits_to_cdf_adversarial_rows_match_oracle(int_models, oracle_mod, name):
+    from sigcomp_amd.gpu_entropy_coding import int8_logits_to_cdf
+    lut = int_models[name].exp_lut
+    rows = _adversarial_logits(np.random.default_rng(11))
+    got = int8_logits_to_cdf(torch.from_numpy(rows).cuda(), lut).cpu().numpy()
+    exp = oracle_mod.logits_to_cdf(rows, lut)
+    assert got.shape == exp.shape
+    bad = np.flatnonzero((got != exp).any(axis=1))
+    assert bad.size == 0, f"rows {bad[:10]} differ"
+
+
 def _golden_streams(name):
     z = np.load(GOLDEN / "coder_streams.npz")
     keys = sorted({k.rsplit("_", 1)[0] for k in z.files if k.startswith(name + "_")})
