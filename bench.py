@@ -15,7 +15,10 @@ decompress time)); compress and decompress rates, bits/sample, the
 roofline of the dominant kernel (k_decompress, int8 MFMA bound) measured
 with HIP events on its own stream, and the CPU oracle baseline on a bounded
 sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c2 = MLP
-microbenchmark (1,048,576 context rows -> int32 CDF tables).
+microbenchmark (1,048,576 context rows -> int32 CDF tables); ceiling = the
+int8 MFMA rate the GPU sustains at its power limit (register-operand MFMA
+chains on every CU, random and zero operands), recorded in
+profiles/mfma_ceiling.txt and quoted beside the 5.0 POP/s spec peak.
 """
 
 from __future__ import annotations
@@ -160,7 +163,8 @@ def bench_codec(args):
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
                      "traffic": pmc_traffic(args.config, "k_decompress"),
                      "traffic_source": f"profiles/traffic_{args.config}.txt (rocprofv3 PMC, bytes per launch)",
-                     "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch"},
+                     "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch",
+                     **ceiling_fields(achieved)},
     }
     return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
 
@@ -315,7 +319,75 @@ def bench_mlp(args):
             "config": {"workload": f"c2: {rows} context rows, random per-channel int8 model"},
             "roofline": {"kernel": "k_mlp_context<cdf>", "bound": "mfma", "achieved": round(achieved, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None}}
+                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                         **ceiling_fields(achieved)}}
+
+
+def bench_ceiling(args):
+    """The int8 MFMA rate the GPU sustains at its power limit: every CU runs
+    register-operand v_mfma_i32_32x32x32_i8 chains (sc_mfma_burn_i8) for
+    about 6 s per operand set (long enough for the power controller to settle)
+    with random int8 operands (the data the codec's MFMAs see) and with
+    zeros (no toggling: close to the clock-limited 5.0 POP/s)."""
+    import time
+
+    import torch
+    from sigcomp_amd import _hip
+    L = _hip.lib()
+    n_groups = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 5000
+    ops_per_launch = n_groups * 4 * iters * 64 * 65536
+    out = torch.empty(n_groups * 256 * 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    g = torch.Generator().manual_seed(1)
+    for name in ("random", "zero"):
+        ops = (torch.randint(-128, 128, (8192,), dtype=torch.int8, generator=g) if name == "random"
+               else torch.zeros(8192, dtype=torch.int8)).cuda()
+        rc = L.sc_mfma_burn_i8(ops.data_ptr(), 10, n_groups, out.data_ptr(), stream)
+        if rc:
+            raise RuntimeError(L.sc_last_error().decode())
+        torch.cuda.synchronize()
+        rates = []
+        t_end = time.time() + 6.0
+        while time.time() < t_end:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            L.sc_mfma_burn_i8(ops.data_ptr(), iters, n_groups, out.data_ptr(), stream)
+            e1.record()
+            torch.cuda.synchronize()
+            rates.append(ops_per_launch / (e0.elapsed_time(e1) / 1e3) / 1e12)
+        # the last second: the steady state under the power limit
+        tail = rates[-max(1, len(rates) // 6):]
+        res[name] = round(float(np.median(tail)), 1)
+        log(f"[bench] MFMA burn, {name} operands: {res[name]} TOP/s (median of the last {len(tail)} launches)")
+    return {"metric": "sustained int8 MFMA rate (register operands, all CUs)", "value": res["random"],
+            "unit": "TOP/s", "n_gpus": 1, "steps": len(rates), "warmup": 1, "ms_per_step": None,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic", "config": {"workload": f"{n_groups} workgroups x 4 waves x {iters * 64} "
+                                                        "v_mfma_i32_32x32x32_i8 per launch"},
+            "zero_operands_tops": res["zero"], "peak": PEAK_INT8_TOPS,
+            "frac_of_peak": round(res["random"] / PEAK_INT8_TOPS, 4)}
+
+
+def power_capped_peak():
+    """Sustained int8 MFMA rate with random operands, measured by
+    `bench.py --config ceiling` and recorded in profiles/mfma_ceiling.txt."""
+    f = REPO / "profiles" / "mfma_ceiling.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("random_operands_tops"):
+            return float(line.split()[1])
+    return None
+
+
+def ceiling_fields(achieved):
+    cap = power_capped_peak()
+    if cap is None:
+        return {}
+    return {"power_capped_peak": cap, "frac_of_power_capped_peak": round(achieved / cap, 4),
+            "power_capped_peak_source": "profiles/mfma_ceiling.txt (bench.py --config ceiling)"}
 
 
 def main():
@@ -323,7 +395,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2", "ceiling"])
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -336,6 +408,9 @@ def main():
         sys.exit(2)
     if args.config == "c2":
         print(json.dumps(bench_mlp(args)), flush=True)
+        return
+    if args.config == "ceiling":
+        print(json.dumps(bench_ceiling(args)), flush=True)
         return
     res, chunks, samples, cfg, gpu_out = bench_codec(args)
     if not args.no_cpu_baseline:

@@ -183,6 +183,15 @@ int sc_compress_chunks(const sc_model *model, const uint8_t *tokens, const int64
 int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt, int64_t n_chunks,
                     uint32_t *out, const int64_t *out_off, void *stream);
 
+/* Measurement hook, no counterpart in the reference: n_groups workgroups of
+ * 4 wavefronts each issue iters * 64 v_mfma_i32_32x32x32_i8 (65,536 int ops
+ * each) on register operands taken from ops (device, 8192 bytes: 4 A and 4 B
+ * fragments of 64 lanes x 16 bytes), with no memory traffic in the loop; out
+ * (device, n_groups * 256 * 16 int32) receives the accumulator sums.  Timed
+ * by the caller, it gives the int8 MFMA rate the GPU sustains at its power
+ * limit for that operand data (the practical ceiling of the MLP kernels). */
+int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t *out, void *stream);
+
 /* Decompress n_chunks chunks with one persistent kernel: every workgroup owns
  * a tile of chunks and runs the whole autoregressive loop for them (MLP step,
  * fused frequency step and decoder step per token, context kept on chip).

@@ -566,6 +566,41 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
     symbols_out[b] = sym;
 }
 
+// ---- measurement: sustained int8 MFMA rate -------------------------------
+// Every wave runs 8 independent accumulator chains of v_mfma_i32_32x32x32_i8
+// on register operands (4 A and 4 B fragments of `ops`, rotated so that
+// consecutive MFMAs see different data; no memory traffic in the loop): the
+// int8 MFMA rate the chip sustains at its power limit for the given operand
+// data, against which the codec kernels' MFMA rate is read.
+__global__ __launch_bounds__(THREADS, 1) void k_mfma_burn(const v4i *__restrict__ ops, int32_t iters,
+                                                          v16i *__restrict__ out) {
+    const int l = threadIdx.x & 63;
+    v4i a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a[j] = ops[j * 64 + l];
+        b[j] = ops[256 + j * 64 + l];
+    }
+    v16i acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = v16i{};
+    for (int32_t it = 0; it < iters; ++it) {
+        static_for<4>([&](auto ic) {
+            constexpr int i2 = decltype(ic)::value;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j & 3], b[(j + i2) & 3], acc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(j + 1) & 3], b[(j + 2 + i2) & 3], acc[j], 0, 0, 0);
+        });
+    }
+    v16i s = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) s += acc[j];
+    out[(int64_t)blockIdx.x * THREADS + threadIdx.x] = s;
+}
+
 }  // namespace
 
 // =========================================================================
@@ -932,6 +967,13 @@ int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_
     hipLaunchKernelGGL(k_gather_words, dim3((unsigned)((n_chunks + WAVES - 1) / WAVES)), dim3(THREADS), 0,
                        as_stream(stream), words, word_off, word_cnt, n_chunks, out, out_off);
     return check_launch("k_gather_words");
+}
+
+int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t *out, void *stream) {
+    if (iters < 0 || n_groups <= 0 || !ops || !out) return fail(SC_ERR_ARG, "bad argument");
+    hipLaunchKernelGGL(k_mfma_burn, dim3((unsigned)n_groups), dim3(THREADS), 0, as_stream(stream),
+                       (const v4i *)ops, iters, (v16i *)out);
+    return check_launch("k_mfma_burn");
 }
 
 int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt,

@@ -288,3 +288,36 @@ def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, units, extra
     chunks = [tokens[off[i]:off[i] + lengths[i]] for i in sample]
     ref = oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
     assert [words[woff[i]:woff[i] + wcnt[i]].tobytes() for i in sample] == ref
+
+
+def test_mfma_burn_hook_computes_its_products():
+    """The power-limit measurement hook (sc_mfma_burn_i8) really issues the
+    MFMAs it is timed for: its accumulator sums equal the int8 matrix
+    products of its fragments, restated with numpy (fragment j of A holds
+    A_j[m][k] at lane m + 32*(k // 16), byte k % 16; B likewise with column n;
+    lane l, register v of the 32x32 result holds row 8*(v//4) + 4*(l//32) +
+    v%4, column l % 32)."""
+    from sigcomp_amd import _hip
+    L = _hip.lib()
+    rng = np.random.default_rng(8)
+    ops = rng.integers(-128, 128, 8192).astype(np.int8)
+    iters, groups = 2, 3
+    out = torch.zeros(groups * 256 * 16, dtype=torch.int32, device="cuda")
+    d_ops = torch.from_numpy(ops).cuda()
+    _hip.check(L.sc_mfma_burn_i8(d_ops.data_ptr(), iters, groups, out.data_ptr(),
+                                 torch.cuda.current_stream().cuda_stream))
+    got = out.cpu().numpy().reshape(groups, 4, 64, 16)
+    frag = ops.reshape(512, 16).astype(np.int64)
+    row = np.arange(32)[:, None]      # A: m, B: k
+    col = np.arange(32)[None, :]      # A: k, B: n
+    A = [frag[j * 64 + row + 32 * (col // 16), col % 16] for j in range(4)]          # A_j[m][k]
+    B = [frag[256 + j * 64 + col + 32 * (row // 16), row % 16] for j in range(4)]    # B_j[k][n]
+    D = np.zeros((32, 32), np.int64)
+    for i2 in range(4):
+        for j in range(8):
+            D += A[j & 3] @ B[(j + i2) & 3] + A[(j + 1) & 3] @ B[(j + 2 + i2) & 3]
+    D = (D * iters).astype(np.int64)
+    lane = np.arange(64)[:, None]
+    v = np.arange(16)[None, :]
+    exp = D[8 * (v // 4) + 4 * (lane // 32) + v % 4, lane % 32].astype(np.int32)
+    assert all(np.array_equal(got[g, w], exp) for g in range(groups) for w in range(4))
