@@ -268,10 +268,12 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
 // addresses one position ahead.
 //
 // General form: n-tile of accumulator j is nt(j), accumulator tile (j, i) is
-// acc(j, i) (a reference); the form below it covers n-tiles nt0 .. nt0+NTP-1.
-template <int NTP, int RT, class TokFn, class NtFn, class AccFn>
+// acc(j, i) (a reference), and the first k-step accumulates onto init(j, i)
+// (zero, a bias tile, or acc(j, i) itself), so the accumulators need no
+// separate initialisation; the form below it covers n-tiles nt0 .. nt0+NTP-1.
+template <int NTP, int RT, class TokFn, class NtFn, class AccFn, class InitFn>
 __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, const uint8_t *s_emb, TokFn tok,
-                                                AccFn acc, int lane) {
+                                                AccFn acc, InitFn init, int lane) {
     constexpr int PD = 4;
     static_assert(WIN % 2 == 0, "positions are processed in pairs");
     int voff[NTP];
@@ -296,8 +298,10 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
     v4i b[2][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_emb + eb[0][i] + ((g ^ ek[0][i]) << 4));
-#pragma unroll 1
-    for (int p0 = 0; p0 < WIN; p0 += 2) {
+    // one pair of positions; the first pair is a separate copy whose first
+    // k-step takes init() as the accumulator input
+    auto pair = [&](int p0, auto firstc) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(firstc)::value;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int p = p0 + h, hn = h ^ 1;
@@ -326,21 +330,27 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
 #pragma unroll
                     for (int i = 0; i < RT; ++i) {
                         v16i &a = acc(j, i);
-                        a = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i], a, 0, 0, 0);
+                        a = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i],
+                                                                  FIRST && h == 0 && s == 0 ? init(j, i) : a,
+                                                                  0, 0, 0);
                     }
                 kstep_schedule<NTP, RT>();
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-    }
+    };
+    pair(0, std::true_type{});
+#pragma unroll 1
+    for (int p0 = 2; p0 < WIN; p0 += 2) pair(p0, std::false_type{});
 }
 
 template <int NTP, int RT, class TokFn>
 __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
                                             TokFn tok, v16i (&acc)[NTP][RT], int lane) {
+    const v16i zero = {};
     gemm_layer0_map<NTP, RT>(
         ws, [&](int j) { return nt0 + j; }, s_emb, tok,
-        [&](int j, int i) -> v16i & { return acc[j][i]; }, lane);
+        [&](int j, int i) -> v16i & { return acc[j][i]; }, [&](int, int) { return zero; }, lane);
 }
 
 // Requantise accumulators to packed int8.  Accumulator element v of tile
@@ -348,7 +358,10 @@ __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const ui
 // row r = i*32 + lane%32, so pk[j][i][g] holds features n0 .. n0+3 with
 // n0 = (nt0 + j)*32 + 8*g + 4*(lane/32).  `par` points at the LDS copy of
 // the parameter block of n-tile nt0.
-template <int NTP, int RT, bool FAST, bool RELU>
+//
+// BIAS = false: the accumulators already hold the bias (their GEMM started
+// from the bias tile), the bias add is skipped.
+template <int NTP, int RT, bool FAST, bool RELU, bool BIAS = true>
 __device__ __forceinline__ void requant_pack_t(const v16i (&acc)[NTP][RT], const uint32_t *par, int lane,
                                                uint32_t (&pk)[NTP][RT][4]) {
     const int g2 = lane >> 5;
@@ -356,12 +369,12 @@ __device__ __forceinline__ void requant_pack_t(const v16i (&acc)[NTP][RT], const
 #pragma unroll
     for (int j = 0; j < NTP; ++j) {
         const uint32_t *pj = par + j * PAR_DWORDS;
-        v4i bb[4], mm[4];
+        v4i bb[4] = {}, mm[4];
         uint32_t sh[4][4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int o = 8 * g + 4 * g2;
-            bb[g] = *(const v4i *)(pj + o);
+            if constexpr (BIAS) bb[g] = *(const v4i *)(pj + o);
             mm[g] = *(const v4i *)(pj + 32 + o);
             const uint32_t ss = pj[64 + (o >> 2)];
 #pragma unroll
@@ -465,7 +478,7 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
         constexpr int pass = decltype(pc)::value;
         const int nt0 = ntw0 + pass * NTP;
         v16i acc[NTP][RT];
-        zero_acc(acc);
+        if constexpr (!FIRST) zero_acc(acc);   // layer 0 starts its accumulators from zero itself
         const WStream ws = make_wstream(L.w, L.bytes);
         if constexpr (FIRST) gemm_layer0<NTP, RT>(ws, nt0, s_emb, tok, acc, lane);
         else gemm_hidden<NTP, RT, KTH>(ws, nt0, s_act, acc, lane);

@@ -38,6 +38,11 @@ __device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb
     if constexpr (PIPE) mlp_rows_pipe<RT>(M, s_emb, s_act, s_par, tok, wave, lane);
     else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, tok, wave, lane);
 }
+// once per kernel, before the first mlp_tile (and a barrier)
+template <bool PIPE>
+__device__ __forceinline__ void mlp_tile_init(const ModelDev &M, uint32_t *s_par, int wave, int lane) {
+    if constexpr (PIPE) pipe_params_init(M, s_par, wave, lane);
+}
 template <bool PIPE>
 constexpr int par_lds_dwords() { return PIPE ? PIPE_PAR_DWORDS : PAR_LDS_DWORDS; }
 // activation row layout of the core: padded rows (pipelined) or swizzled rows
@@ -60,6 +65,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<PIPE>(M, s_par, wave, lane);
     const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
     for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         const int64_t row0 = tile * R_TILE;
@@ -168,6 +174,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<PIPE>(M, s_par, wave, lane);
     const int32_t n_tiles = tile_start[n_chunks];
     for (int32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         __syncthreads();
@@ -287,6 +294,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     const int64_t c0 = (int64_t)blockIdx.x * R;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<PIPE>(M, s_par, wave, lane);
     if (threadIdx.x == 0) s_maxlen = 0;
     __syncthreads();
     for (int r = threadIdx.x; r < R; r += THREADS) {

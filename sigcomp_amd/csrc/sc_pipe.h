@@ -33,13 +33,39 @@ constexpr int PNT = 2;                               // n-tiles per pass
 constexpr int PPD = 4;                               // weight prefetch distance (k-steps)
 constexpr int PBLK = PNT * PAR_DWORDS;               // parameter dwords of one pass
 constexpr int PBLK_LANE = (PBLK + 63) / 64;
-// LDS parameter slots per wave: 0 = pass 0 of the current layer, 1 and 2 =
-// pass 1 of even / odd layers (read while the next layer runs).
-constexpr int PIPE_PAR_DWORDS = WAVES * 3 * PBLK;
+// LDS parameter slots per wave: slot_p0(l) holds the pass-0 parameter blocks
+// of layer l, slot_p1(l) its pass-1 blocks.  Layers l >= 1 use four slots by
+// parity: layer l's pass-0 blocks are written during layer l-1 (layer l's
+// first MFMAs start from their bias tiles), its pass-1 blocks during layer l
+// (read until layer l+1 has requantised layer l's pass 1).  Layer 0's two
+// slots are written once per kernel (pipe_params_init), before the first MLP
+// evaluation, so that its bias tiles are in LDS when each evaluation starts.
+constexpr int PIPE_SLOTS = 6;
+constexpr int PIPE_PAR_DWORDS = WAVES * PIPE_SLOTS * PBLK;
+__device__ __forceinline__ int slot_p0(int l) { return l == 0 ? 4 : (l & 1); }
+__device__ __forceinline__ int slot_p1(int l) { return l == 0 ? 5 : 2 + (l & 1); }
 
-// Requant parameters of packed group g of n-tile j (lane half g2).
+// Bias of n-tile j of a parameter block as an accumulator tile: element v of
+// a lane in half g (= lane / 32) is the bias of feature 8*(v/4) + 4*g + v%4,
+// the feature that accumulator element holds.  A GEMM whose first MFMA
+// accumulates onto it ends with acc + bias (int32, wrapping like the
+// reference's add), so the requantisation skips the bias add.
+__device__ __forceinline__ v16i bias_tile(const uint32_t *blk, int j, int g) {
+    const uint32_t *pj = blk + j * PAR_DWORDS + 4 * g;
+    v16i t;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+        const v4i x = *(const v4i *)(pj + 8 * gg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[4 * gg + e] = x[e];
+    }
+    return t;
+}
+
+// Requant parameters (M0 and shift; the bias is already in the accumulators)
+// of packed group g of n-tile j (lane half g2).
 struct RqPar {
-    v4i bb, mm;
+    v4i mm;
     uint32_t sh;
 };
 
@@ -47,20 +73,20 @@ __device__ __forceinline__ RqPar rq_par(const uint32_t *blk, int j, int g, int g
     const uint32_t *pj = blk + j * PAR_DWORDS;
     const int o = 8 * g + 4 * g2;
     RqPar p;
-    p.bb = *(const v4i *)(pj + o);
     p.mm = *(const v4i *)(pj + 32 + o);
     p.sh = pj[64 + (o >> 2)];
     return p;
 }
 
-// Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile -> packed int8.
+// Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile (bias included)
+// -> packed int8.
 template <bool RELU>
 __device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar &p) {
     constexpr int lo = RELU ? 0 : -128;
     uint32_t packed = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const uint32_t q = requant_u8_fast(acc[4 * g + e], p.bb[e], p.mm[e], (p.sh >> (8 * e)) & 63u, lo);
+        const uint32_t q = requant_u8_fast(acc[4 * g + e], 0, p.mm[e], (p.sh >> (8 * e)) & 63u, lo);
         packed |= q << (8 * e);
     }
     return packed;
@@ -88,6 +114,17 @@ __device__ __forceinline__ void par_put(uint32_t *blk, const uint32_t (&pr)[PBLK
 #pragma unroll
     for (int d = 0; d < PBLK_LANE; ++d)
         if (d * 64 + lane < PBLK) blk[d * 64 + lane] = pr[d];
+}
+
+// Layer 0's parameter blocks (read by every MLP evaluation of the kernel)
+// into their slots; the caller's next barrier makes them visible.
+__device__ __forceinline__ void pipe_params_init(const ModelDev &M, uint32_t *s_par, int wave, int lane) {
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * PBLK;
+    uint32_t pr[PBLK_LANE];
+    par_fetch(M.layer[0].par, 2 * wave, lane, pr);
+    par_put(s_parw + slot_p0(0) * PBLK, pr, lane);
+    par_fetch(M.layer[0].par, 8 + 2 * wave, lane, pr);
+    par_put(s_parw + slot_p1(0) * PBLK, pr, lane);
 }
 
 // Activation rows of the pipelined core are padded to PACT_ROW bytes instead
@@ -144,19 +181,20 @@ __device__ __forceinline__ void pipe_schedule() {
     });
 }
 
-// One hidden layer (LASTL = false) or the output layer (LASTL = true, one
+// One hidden layer l (LASTL = false) or the output layer (LASTL = true, one
 // pass: n-tiles 2w, 2w+1 = logits 64w .. 64w+63, stored in natural order).
-// Entry: accB = layer l-1 pass 1 (not yet requantised, parameters in slot
-// `prev_slot`), region A = layer l-1 pass 0 (visible to all waves),
-// w[0][*] = this layer's first PPD weight k-steps.  Exit: accB = this
-// layer's pass 1, slot `cur_slot` = its parameters, region A = this layer's
-// pass 0 (visible), w[0][*] = the next layer's first k-steps.
+// Entry: accB = layer l-1 pass 1 (bias included, not yet requantised,
+// parameters in slot_p1(l-1)), region A = layer l-1 pass 0 (visible to all
+// waves), slot_p0(l) = this layer's pass-0 parameters, w[0][*] = this
+// layer's first PPD weight k-steps.  Exit: accB = this layer's pass 1,
+// slot_p1(l) = its parameters, slot_p0(l+1) = the next layer's pass-0
+// parameters, region A = this layer's pass 0 (visible), w[0][*] = the next
+// layer's first k-steps.  Both passes' GEMMs start from their bias tiles.
 template <int RT, bool LASTL>
 __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
-                                            uint32_t *s_parw, int prev_slot, int cur_slot,
-                                            v16i (&accA)[PNT][RT], v16i (&accB)[PNT][RT],
-                                            v4i (&w)[2][PPD][PNT], uint32_t (&pk)[PNT][RT][4], int wave,
-                                            int lane) {
+                                            uint32_t *s_parw, int l, v16i (&accA)[PNT][RT],
+                                            v16i (&accB)[PNT][RT], v4i (&w)[2][PPD][PNT],
+                                            uint32_t (&pk)[PNT][RT][4], int wave, int lane) {
     constexpr int NV = LASTL ? KTH : 2 * KTH;
     constexpr int MF = PNT * RT;
     constexpr int RH = (RT + 1) / 2;          // row tiles requantised in the first of two steps
@@ -165,16 +203,21 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
     const __amdgpu_buffer_rsrc_t rs = layer_rsrc(L);
     const __amdgpu_buffer_rsrc_t rsn = layer_rsrc(Ln);
     const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;   // n-tile bases of pass 0 / pass 1
-    const uint32_t *prev = s_parw + prev_slot * PBLK;
-    uint32_t *blk0 = s_parw;
-    uint32_t *blkc = s_parw + cur_slot * PBLK;
-    uint32_t pr0[PBLK_LANE], pr1[PBLK_LANE];
-    par_fetch(L.par, nb0, lane, pr0);
-    if constexpr (!LASTL) par_fetch(L.par, nb1, lane, pr1);
+    const uint32_t *prev1 = s_parw + slot_p1(l - 1) * PBLK;
+    const uint32_t *cur0 = s_parw + slot_p0(l) * PBLK;
+    uint32_t *cur1 = s_parw + slot_p1(l) * PBLK;
+    uint32_t *next0 = s_parw + slot_p0(l + 1) * PBLK;
+    uint32_t pr1[PBLK_LANE], prn[PBLK_LANE];
+    if constexpr (!LASTL) {
+        par_fetch(L.par, nb1, lane, pr1);
+        par_fetch(Ln.par, nb0, lane, prn);
+    }
     v4i b[2][RT];
     read_b<RT>(s_act, bbase, 0, b[0]);
-    RqPar pp = rq_par(prev, 0, 0, g);
-    const v16i zero = {};
+    RqPar pp = rq_par(prev1, 0, 0, g);
+    v16i bias[PNT];
+#pragma unroll
+    for (int j = 0; j < PNT; ++j) bias[j] = bias_tile(cur0, j, g);
     static_for<NV>([&](auto vc) __attribute__((always_inline)) {
         constexpr int v = decltype(vc)::value;
         constexpr int pass = v / KTH, kt = v % KTH, set = (v / PPD) & 1, slot = v % PPD;
@@ -198,15 +241,20 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
         if constexpr (v < 8) {
             constexpr int j = v / 4, gg = v % 4;
             const RqPar cur = pp;
-            if constexpr (v + 1 < 8) pp = rq_par(prev, (v + 1) / 4, (v + 1) % 4, g);
+            if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
 #pragma unroll
             for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
         } else if constexpr (!LASTL && v >= 16) {
             constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
             const RqPar cur = pp;
-            if constexpr (u + 1 < 16) pp = rq_par(blk0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
+            if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
 #pragma unroll
             for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
+        }
+        // pass 1's bias tiles, one step before its first MFMAs
+        if constexpr (!LASTL && v == KTH - 1) {
+#pragma unroll
+            for (int j = 0; j < PNT; ++j) bias[j] = bias_tile(cur1, j, g);
         }
         // this step's MFMAs
         auto &acc = pass == 0 ? accA : accB;
@@ -215,23 +263,24 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
 #pragma unroll
             for (int i = 0; i < RT; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[set][slot][j], b[kt & 1][i],
-                                                                  kt == 0 ? zero : acc[j][i], 0, 0, 0);
-        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 3, PNT, VA>();
+                                                                  kt == 0 ? bias[j] : acc[j][i], 0, 0, 0);
+        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 2 + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (v == 7) {
-            // layer l-1 pass 1 -> region B; this layer's parameters -> LDS
+            // layer l-1 pass 1 -> region B; this layer's pass-1 and the next
+            // layer's pass-0 parameters -> LDS
             pstore_perm<RT>(pk, nb1, s_act, lane);
-            par_put(blk0, pr0, lane);
             if constexpr (!LASTL) {
-                par_put(blkc, pr1, lane);
-                pp = rq_par(blk0, 0, 0, g);   // first parameters of the pass-0 requantisation
+                par_put(cur1, pr1, lane);
+                par_put(next0, prn, lane);
+                pp = rq_par(cur0, 0, 0, g);   // first parameters of the pass-0 requantisation
             }
             __syncthreads();
             read_b<RT>(s_act, bbase, 8, b[0]);
         }
     });
     if constexpr (LASTL) {
-        requant_pack_t<PNT, RT, true, false>(accA, blk0, lane, pk);
+        requant_pack_t<PNT, RT, true, false, false>(accA, cur0, lane, pk);
         __syncthreads();
         pstore_natural<RT>(pk, nb0, s_act, lane);
     } else {
@@ -244,7 +293,8 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
 // One MLP evaluation of R = 32*RT rows (RT <= 4), same contract as mlp_rows
 // but in the padded row layout: entered after a barrier that ends every read
 // of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of
-// each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS.
+// each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS,
+// layer 0's slots filled by pipe_params_init.
 template <int RT, class TokFn>
 __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
                                               uint32_t *s_par, TokFn tok, int wave, int lane) {
@@ -255,28 +305,34 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     wave = __builtin_amdgcn_readfirstlane(wave);
     const int voff = lane * 16;
     const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;
-    uint32_t *s_parw = s_par + wave * 3 * PBLK;
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * PBLK;
     v16i accA[PNT][RT], accB[PNT][RT];
     v4i w[2][PPD][PNT];
     uint32_t pk[PNT][RT][4];
     // layer 0 in one pass over both passes' n-tiles (each embedding B
-    // fragment is read from LDS once), then the pass-0 requantisation and
-    // store (no wave reads s_act during layer 0); pass 1 stays in accB for
-    // the first hidden layer; then that layer's first weights
+    // fragment is read from LDS once), starting from the bias tiles, then
+    // the pass-0 requantisation and store (no wave reads s_act during layer
+    // 0); pass 1 stays in accB for the first hidden layer; then that layer's
+    // pass-0 parameters and first weights
     {
         const LayerDev &L0 = M.layer[0];
-        uint32_t pr0[PBLK_LANE], pr1[PBLK_LANE];
-        par_fetch(L0.par, nb0, lane, pr0);
-        par_fetch(L0.par, nb1, lane, pr1);
+        const int g = lane >> 5;
+        const uint32_t *p00 = s_parw + slot_p0(0) * PBLK, *p10 = s_parw + slot_p1(0) * PBLK;
+        uint32_t prn[PBLK_LANE];
+        par_fetch(M.layer[1].par, nb0, lane, prn);
+        v16i bias[2 * PNT];
+#pragma unroll
+        for (int j = 0; j < PNT; ++j) {
+            bias[j] = bias_tile(p00, j, g);
+            bias[PNT + j] = bias_tile(p10, j, g);
+        }
         const WStream ws = make_wstream(L0.w, L0.bytes);
-        zero_acc(accA);
-        zero_acc(accB);
         gemm_layer0_map<2 * PNT, RT>(
             ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, tok,
-            [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; }, lane);
-        par_put(s_parw, pr0, lane);
-        par_put(s_parw + 1 * PBLK, pr1, lane);
-        requant_pack_t<PNT, RT, true, true>(accA, s_parw, lane, pk);
+            [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; },
+            [&](int j, int) { return bias[j]; }, lane);
+        par_put(s_parw + slot_p0(1) * PBLK, prn, lane);
+        requant_pack_t<PNT, RT, true, true, false>(accA, p00, lane, pk);
         pstore_perm<RT>(pk, nb0, s_act, lane);
         const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
 #pragma unroll
@@ -288,10 +344,8 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     const int last = M.n_layers - 1;
 #pragma unroll 1
     for (int l = 1; l < last; ++l)
-        pipe_hidden<RT, false>(M.layer[l], M.layer[l + 1], s_act, s_parw, 1 + ((l - 1) & 1), 1 + (l & 1), accA,
-                               accB, w, pk, wave, lane);
-    pipe_hidden<RT, true>(M.layer[last], M.layer[last], s_act, s_parw, 1 + ((last - 1) & 1), 0, accA, accB, w, pk,
-                          wave, lane);
+        pipe_hidden<RT, false>(M.layer[l], M.layer[l + 1], s_act, s_parw, l, accA, accB, w, pk, wave, lane);
+    pipe_hidden<RT, true>(M.layer[last], M.layer[last], s_act, s_parw, last, accA, accB, w, pk, wave, lane);
 }
 
 }  // namespace sc
