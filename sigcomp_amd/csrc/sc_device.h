@@ -264,15 +264,17 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
 // Layer 0: the B operand row r, k = p*128 + j is emb[tok(r, p)][j], gathered
 // from the LDS embedding table; a k-tile of 32 never straddles a position,
 // so a position is PD = 4 k-steps.  Same pipeline as gemm_hidden over pairs
-// of positions; tokens are read two positions ahead and turned into table
-// addresses one position ahead.
+// of positions.  apos(r, p) = emb_off(tok(r, p), 0), the table address of
+// the token's chunk 0 (the callers keep tokens in that form): chunk c of the
+// token is at apos ^ (c << 4), so a lane's chunk 2q + g of a position is one
+// XOR away from apos ^ (g << 4).  Addresses are read two positions ahead.
 //
 // General form: n-tile of accumulator j is nt(j), accumulator tile (j, i) is
 // acc(j, i) (a reference), and the first k-step accumulates onto init(j, i)
 // (zero, a bias tile, or acc(j, i) itself), so the accumulators need no
 // separate initialisation; the form below it covers n-tiles nt0 .. nt0+NTP-1.
-template <int NTP, int RT, class TokFn, class NtFn, class AccFn, class InitFn>
-__device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, const uint8_t *s_emb, TokFn tok,
+template <int NTP, int RT, class AposFn, class NtFn, class AccFn, class InitFn>
+__device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, const uint8_t *s_emb, AposFn apos,
                                                 AccFn acc, InitFn init, int lane) {
     constexpr int PD = 4;
     static_assert(WIN % 2 == 0, "positions are processed in pairs");
@@ -284,20 +286,19 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
     for (int s = 0; s < PD; ++s)
 #pragma unroll
         for (int j = 0; j < NTP; ++j) w[0][s][j] = wload(ws, voff[j], s);
-    const int rl = lane & 31, g = lane >> 5;
-    // eb/ek[x]: table row offset and swizzle key of the position with parity x;
-    // tk[x]: raw tokens of the next unconverted position with parity x
-    int eb[2][RT], ek[2][RT], tk[2][RT];
+    const int rl = lane & 31, kg = (lane >> 5) << 4;
+    // ea[x]: address of this lane's chunk g of the position with parity x
+    // (chunk 2q + g is at ea ^ (q << 5)); an[x]: apos of the next position
+    // with parity x
+    int ea[2][RT], an[2][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-        const int t = tok(i * 32 + rl, 0);
-        eb[0][i] = t * EDIM;
-        ek[0][i] = t & 7;
-        tk[1][i] = tok(i * 32 + rl, 1);
+        ea[0][i] = apos(i * 32 + rl, 0) ^ kg;
+        an[1][i] = apos(i * 32 + rl, 1);
     }
     v4i b[2][RT];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_emb + eb[0][i] + ((g ^ ek[0][i]) << 4));
+    for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_emb + ea[0][i]);
     // one pair of positions; the first pair is a separate copy whose first
     // k-step takes init() as the accumulator input
     auto pair = [&](int p0, auto firstc) __attribute__((always_inline)) {
@@ -308,9 +309,8 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
             const int p2 = p + 2 < WIN ? p + 2 : WIN - 1;
 #pragma unroll
             for (int i = 0; i < RT; ++i) {
-                eb[hn][i] = tk[hn][i] * EDIM;      // position p + 1
-                ek[hn][i] = tk[hn][i] & 7;
-                tk[h][i] = tok(i * 32 + rl, p2);   // position p + 2
+                ea[hn][i] = an[hn][i] ^ kg;         // position p + 1
+                an[h][i] = apos(i * 32 + rl, p2);   // position p + 2
             }
 #pragma unroll
             for (int s = 0; s < PD; ++s) {
@@ -318,10 +318,8 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
                 const int bc = s & 1, bn = bc ^ 1;
 #pragma unroll
                 for (int i = 0; i < RT; ++i) {
-                    const int base = s + 1 < PD ? eb[h][i] : eb[hn][i];
-                    const int k2 = s + 1 < PD ? ek[h][i] : ek[hn][i];
-                    const int c = ((s + 1) % PD) * 2 + g;
-                    b[bn][i] = *(const v4i *)(s_emb + base + ((c ^ k2) << 4));
+                    const int e = s + 1 < PD ? ea[h][i] : ea[hn][i];
+                    b[bn][i] = *(const v4i *)(s_emb + (e ^ (((s + 1) % PD) << 5)));
                 }
 #pragma unroll
                 for (int j = 0; j < NTP; ++j) w[hn][s][j] = wload(ws, voff[j], kt + PD);
@@ -344,12 +342,12 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
     for (int p0 = 2; p0 < WIN; p0 += 2) pair(p0, std::false_type{});
 }
 
-template <int NTP, int RT, class TokFn>
+template <int NTP, int RT, class AposFn>
 __device__ __forceinline__ void gemm_layer0(const WStream &ws, int nt0, const uint8_t *s_emb,
-                                            TokFn tok, v16i (&acc)[NTP][RT], int lane) {
+                                            AposFn apos, v16i (&acc)[NTP][RT], int lane) {
     const v16i zero = {};
     gemm_layer0_map<NTP, RT>(
-        ws, [&](int j) { return nt0 + j; }, s_emb, tok,
+        ws, [&](int j) { return nt0 + j; }, s_emb, apos,
         [&](int j, int i) -> v16i & { return acc[j][i]; }, [&](int, int) { return zero; }, lane);
 }
 
@@ -458,9 +456,9 @@ __device__ __forceinline__ void store_packed_perm(const uint32_t (&pk)[NTP][RT][
 // the layer input, then written over it.  The wave's requant parameter
 // blocks are loaded before its GEMM and copied to its LDS slot `s_par`
 // afterwards.  Leaves with a barrier.
-template <int NTP, int PASSES, int RT, bool FIRST, bool LAST, class TokFn>
+template <int NTP, int PASSES, int RT, bool FIRST, bool LAST, class AposFn>
 __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_emb, uint8_t *s_act,
-                                          uint32_t *s_par, TokFn tok, int wave, int lane) {
+                                          uint32_t *s_par, AposFn apos, int wave, int lane) {
     constexpr int NTW = NTP * PASSES;                 // n-tiles per wave
     constexpr int PW = NTW * PAR_DWORDS;              // parameter dwords per wave
     constexpr int PL = (PW + 63) / 64;                // per lane
@@ -480,7 +478,7 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
         v16i acc[NTP][RT];
         if constexpr (!FIRST) zero_acc(acc);   // layer 0 starts its accumulators from zero itself
         const WStream ws = make_wstream(L.w, L.bytes);
-        if constexpr (FIRST) gemm_layer0<NTP, RT>(ws, nt0, s_emb, tok, acc, lane);
+        if constexpr (FIRST) gemm_layer0<NTP, RT>(ws, nt0, s_emb, apos, acc, lane);
         else gemm_hidden<NTP, RT, KTH>(ws, nt0, s_act, acc, lane);
         if constexpr (pass == 0) {
 #pragma unroll
@@ -503,16 +501,16 @@ __device__ __forceinline__ void mlp_layer(const LayerDev &L, const uint8_t *s_em
 // activations use the store_packed_perm order).  Must be entered after a barrier
 // that ends every read of s_act; leaves with a barrier.  HP = passes per
 // hidden layer (1: 4 n-tiles per pass; 2: 2 n-tiles per pass, fewer registers).
-template <int RT, int HP, class TokFn>
+template <int RT, int HP, class AposFn>
 __device__ __forceinline__ void mlp_rows(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
-                                         uint32_t *s_par, TokFn tok, int wave, int lane) {
+                                         uint32_t *s_par, AposFn apos, int wave, int lane) {
     static_assert(WAVES * 4 * 32 == HID && WAVES * 2 * 32 == VOCAB, "tile split assumes 4 waves");
     constexpr int HN = 4 / HP;
-    mlp_layer<HN, HP, RT, true, false>(M.layer[0], s_emb, s_act, s_par, tok, wave, lane);
+    mlp_layer<HN, HP, RT, true, false>(M.layer[0], s_emb, s_act, s_par, apos, wave, lane);
 #pragma unroll 1
     for (int l = 1; l < M.n_layers - 1; ++l)
-        mlp_layer<HN, HP, RT, false, false>(M.layer[l], s_emb, s_act, s_par, tok, wave, lane);
-    mlp_layer<2, 1, RT, false, true>(M.layer[M.n_layers - 1], s_emb, s_act, s_par, tok, wave, lane);
+        mlp_layer<HN, HP, RT, false, false>(M.layer[l], s_emb, s_act, s_par, apos, wave, lane);
+    mlp_layer<2, 1, RT, false, true>(M.layer[M.n_layers - 1], s_emb, s_act, s_par, apos, wave, lane);
 }
 
 // ---------------------------------------------------------------- frequencies

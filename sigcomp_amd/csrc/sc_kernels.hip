@@ -32,11 +32,11 @@ constexpr int DEC_RT_MAX = 6;       // decode: up to 192 chunks per workgroup
 enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
 
 // MLP core of one tile: the pipelined core when the model allows it.
-template <bool PIPE, int RT, class TokFn>
+template <bool PIPE, int RT, class AposFn>
 __device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act, uint32_t *s_par,
-                                         TokFn tok, int wave, int lane) {
-    if constexpr (PIPE) mlp_rows_pipe<RT>(M, s_emb, s_act, s_par, tok, wave, lane);
-    else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, tok, wave, lane);
+                                         AposFn apos, int wave, int lane) {
+    if constexpr (PIPE) mlp_rows_pipe<RT>(M, s_emb, s_act, s_par, apos, wave, lane);
+    else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, apos, wave, lane);
 }
 // once per kernel, before the first mlp_tile (and a barrier)
 template <bool PIPE>
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
                 v = ctx[row * WIN + (i % WIN)];
                 if (v < 0 || v > SOS) { bad = 1; v = 0; }
             }
-            s_ctx[i] = (uint16_t)v;
+            s_ctx[i] = (uint16_t)emb_off((int)v, 0);   // the MLP takes table addresses
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
@@ -168,6 +168,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ uint16_t s_tok[R_TILE + WIN];
+    __shared__ uint16_t s_apos[R_TILE + WIN];   // emb_off(s_tok[i], 0)
     __shared__ double s_lut[VOCAB];
     __shared__ int64_t s_chunk;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -197,10 +198,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
         // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
         for (int i = threadIdx.x; i < R_TILE + WIN; i += THREADS) {
             const int32_t pos = t0 - WIN + i;
-            s_tok[i] = pos < 0 ? (uint16_t)SOS : (pos < L ? (uint16_t)tk[pos] : (uint16_t)0);
+            const int v = pos < 0 ? SOS : (pos < L ? (int)tk[pos] : 0);
+            s_tok[i] = (uint16_t)v;
+            s_apos[i] = (uint16_t)emb_off(v, 0);
         }
         __syncthreads();
-        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_tok[r + p]; },
+        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
                                 wave, lane);
         const int32_t valid = min(R_TILE, L - t0);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.  The
@@ -282,6 +285,9 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
+    // the pipelined core also keeps the ring as embedding-table addresses
+    // (emb_off(token, 0)), written with the token; the plain core converts
+    __shared__ __attribute__((aligned(16))) uint16_t s_apos[PIPE ? R * WIN : 1];
     __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
@@ -328,7 +334,10 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     for (int32_t t = 0; t < maxlen; ++t) {
         mlp_tile<PIPE, RT>(M, s_emb, s_act, s_par,
                            [&](int r, int p) {
-                               return (t + p < WIN) ? SOS : (int)s_ring[r * WIN + ((t + p) & (WIN - 1))];
+                               const int q = r * WIN + ((t + p) & (WIN - 1));
+                               if (t + p < WIN) return emb_off(SOS, 0);
+                               if constexpr (PIPE) return (int)s_apos[q];
+                               else return emb_off(s_ring[q], 0);
                            },
                            wave, lane);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
@@ -391,6 +400,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                     s_point[r] = pt;
                     s_rpos[r] = rp;
                     s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)(owner * 16 + u);
+                    if constexpr (PIPE) s_apos[r * WIN + (t & (WIN - 1))] = (uint16_t)emb_off(owner * 16 + u, 0);
                 }
                 if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
             }

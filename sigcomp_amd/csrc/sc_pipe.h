@@ -295,9 +295,9 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
 // of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of
 // each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS,
 // layer 0's slots filled by pipe_params_init.
-template <int RT, class TokFn>
+template <int RT, class AposFn>
 __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
-                                              uint32_t *s_par, TokFn tok, int wave, int lane) {
+                                              uint32_t *s_par, AposFn apos, int wave, int lane) {
     static_assert(RT >= 1 && RT <= 4, "two passes of accumulators must fit the AGPRs");
     static_assert(WAVES * 2 * PNT * 32 == HID && WAVES * PNT * 32 == VOCAB, "tile split assumes 4 waves");
     // wave-uniform in a scalar register: weight offsets go to the scalar
@@ -328,7 +328,7 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
         }
         const WStream ws = make_wstream(L0.w, L0.bytes);
         gemm_layer0_map<2 * PNT, RT>(
-            ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, tok,
+            ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, apos,
             [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; },
             [&](int j, int) { return bias[j]; }, lane);
         par_put(s_parw + slot_p0(1) * PBLK, prn, lane);
