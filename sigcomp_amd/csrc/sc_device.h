@@ -33,7 +33,8 @@ constexpr int THREADS = WAVES * 64;
 constexpr int MAX_LAYERS = 16;
 constexpr uint32_t TOTAL = 1u << 24;    // frequency precision 2**24
 constexpr int ACT_ROW = 512;            // bytes per activation row in LDS
-constexpr int EMB_BYTES = EMB_ROWS * EDIM;
+constexpr int EMB_STRIDE = EDIM + 16;   // bytes per embedding row in LDS (see emb_off)
+constexpr int EMB_BYTES = EMB_ROWS * EMB_STRIDE;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -70,10 +71,12 @@ __device__ __forceinline__ int act_off(int r, int chunk) {
     return r * ACT_ROW + ((chunk ^ (r & 15)) << 4);
 }
 
-// Embedding rows: 128 bytes per token, chunks swizzled with the token's low 3 bits.
-__device__ __forceinline__ int emb_off(int tok, int chunk) {
-    return tok * EDIM + ((chunk ^ (tok & 7)) << 4);
-}
+// Embedding rows: 128 bytes per token at a stride of 144 bytes, so that
+// chunk c of token t starts at 9*t + c 16-byte units: lanes reading chunk c
+// of different tokens spread over the bank groups, and the chunks of one
+// token stay in order (chunk c is a constant c*16 bytes from the row start,
+// an immediate of the LDS instruction).
+__device__ __forceinline__ int emb_off(int tok, int chunk) { return tok * EMB_STRIDE + chunk * 16; }
 
 __device__ __forceinline__ void load_emb_lds(const int8_t *__restrict__ emb, uint8_t *s_emb) {
     for (int idx = threadIdx.x; idx < EMB_ROWS * (EDIM / 16); idx += blockDim.x) {
@@ -156,6 +159,16 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 
 // ---------------------------------------------------------------- MFMA GEMMs
+
+// s_waitcnt until at most VM vector-memory and LG LDS/scalar-memory
+// operations of this wave are outstanding (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14, expcnt 6:4 left at its maximum, lgkmcnt 11:8).  The compiler's
+// own waits still guard every use; this only merges them.
+template <int VM, int LG>
+__device__ __forceinline__ void wait_counts() {
+    static_assert(VM >= 0 && VM < 64 && LG >= 0 && LG < 16, "counter range");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LG << 8));
+}
 
 template <int NTP, int RT>
 __device__ __forceinline__ void zero_acc(v16i (&acc)[NTP][RT]) {
@@ -265,9 +278,11 @@ __device__ __forceinline__ void gemm_hidden(const WStream &ws, int nt0, const ui
 // from the LDS embedding table; a k-tile of 32 never straddles a position,
 // so a position is PD = 4 k-steps.  Same pipeline as gemm_hidden over pairs
 // of positions.  apos(r, p) = emb_off(tok(r, p), 0), the table address of
-// the token's chunk 0 (the callers keep tokens in that form): chunk c of the
-// token is at apos ^ (c << 4), so a lane's chunk 2q + g of a position is one
-// XOR away from apos ^ (g << 4).  Addresses are read two positions ahead.
+// the token's row (the callers keep tokens in that form): a lane's chunk
+// 2q + g of a position is at apos + 16 g + 32 q.  Addresses are read two
+// positions ahead.  Each k-step starts with one wait for its own weight
+// fragments and B fragments (loads complete in order), instead of one wait
+// per first use.
 //
 // General form: n-tile of accumulator j is nt(j), accumulator tile (j, i) is
 // acc(j, i) (a reference), and the first k-step accumulates onto init(j, i)
@@ -288,12 +303,12 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
         for (int j = 0; j < NTP; ++j) w[0][s][j] = wload(ws, voff[j], s);
     const int rl = lane & 31, kg = (lane >> 5) << 4;
     // ea[x]: address of this lane's chunk g of the position with parity x
-    // (chunk 2q + g is at ea ^ (q << 5)); an[x]: apos of the next position
-    // with parity x
+    // (chunk 2q + g is at ea + 32 q); an[x]: apos of the next position with
+    // parity x
     int ea[2][RT], an[2][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-        ea[0][i] = apos(i * 32 + rl, 0) ^ kg;
+        ea[0][i] = apos(i * 32 + rl, 0) + kg;
         an[1][i] = apos(i * 32 + rl, 1);
     }
     v4i b[2][RT];
@@ -308,18 +323,21 @@ __device__ __forceinline__ void gemm_layer0_map(const WStream &ws, NtFn nt, cons
             const int p = p0 + h, hn = h ^ 1;
             const int p2 = p + 2 < WIN ? p + 2 : WIN - 1;
 #pragma unroll
-            for (int i = 0; i < RT; ++i) {
-                ea[hn][i] = an[hn][i] ^ kg;         // position p + 1
-                an[h][i] = apos(i * 32 + rl, p2);   // position p + 2
-            }
+            for (int i = 0; i < RT; ++i) ea[hn][i] = an[hn][i] + kg;   // position p + 1
 #pragma unroll
             for (int s = 0; s < PD; ++s) {
                 const int kt = p * PD + s;
                 const int bc = s & 1, bn = bc ^ 1;
+                // this step's weights (issued PD steps ago, NTP per step) and B fragments
+                wait_counts<NTP * (PD - 1), 0>();
+                if (s == 0) {
+#pragma unroll
+                    for (int i = 0; i < RT; ++i) an[h][i] = apos(i * 32 + rl, p2);   // position p + 2
+                }
 #pragma unroll
                 for (int i = 0; i < RT; ++i) {
                     const int e = s + 1 < PD ? ea[h][i] : ea[hn][i];
-                    b[bn][i] = *(const v4i *)(s_emb + (e ^ (((s + 1) % PD) << 5)));
+                    b[bn][i] = *(const v4i *)(s_emb + e + ((s + 1) % PD) * 32);
                 }
 #pragma unroll
                 for (int j = 0; j < NTP; ++j) w[hn][s][j] = wload(ws, voff[j], kt + PD);

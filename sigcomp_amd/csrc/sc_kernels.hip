@@ -22,7 +22,7 @@ namespace {
 
 constexpr int RT_TILE = 4;          // rows per MLP tile = 32 * RT_TILE = 128
 constexpr int R_TILE = 32 * RT_TILE;
-constexpr int DEC_RT_MAX = 6;       // decode: up to 192 chunks per workgroup
+constexpr int DEC_RT_MAX = 5;       // decode: up to 160 chunks per workgroup (LDS)
 
 // Rows of a tile are post-processed four at a time per wavefront: row
 // 4*gi + lane/16 is handled by the 16-lane row lane/16 (see Freq16).
@@ -271,6 +271,12 @@ __global__ __launch_bounds__(256) void k_encode_pairs(const uint2 *__restrict__ 
 // windows (kept as 64-token rings in LDS), the fused frequency step and one
 // decoder step per chunk; the decoded token is appended to the ring.  Chunks
 // are independent, so workgroups never synchronise with each other.
+// Coder state of one chunk between the step segments of a decode.
+struct DecState {
+    uint64_t lower, range, point;
+    int32_t rpos, stat;
+};
+
 template <int RT, bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
                                                            const int64_t *__restrict__ word_off,
@@ -278,7 +284,9 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                                            const int32_t *__restrict__ lengths,
                                                            int64_t n_chunks, uint8_t *__restrict__ tokens,
                                                            const int64_t *__restrict__ tok_off,
-                                                           int32_t *__restrict__ status) {
+                                                           int32_t *__restrict__ status,
+                                                           DecState *__restrict__ state, int32_t t_begin,
+                                                           int32_t t_end) {
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
     static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
@@ -313,25 +321,51 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
             woff = word_off[c];
             toff = tok_off[c];
         }
-        // CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474)
-        uint64_t point = 0;
-        const int take = cnt < 2 ? cnt : 2;
-        for (int i = 0; i < take; ++i) point = (point << 32) | words[woff + i];
-        if (cnt == 1) point <<= 32;
-        s_lower[r] = 0ull;
-        s_range[r] = ~0ull;
-        s_point[r] = point;
-        s_rpos[r] = take;
+        if (t_begin == 0 || c >= n_chunks) {
+            // CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474)
+            uint64_t point = 0;
+            const int take = cnt < 2 ? cnt : 2;
+            for (int i = 0; i < take; ++i) point = (point << 32) | words[woff + i];
+            if (cnt == 1) point <<= 32;
+            s_lower[r] = 0ull;
+            s_range[r] = ~0ull;
+            s_point[r] = point;
+            s_rpos[r] = take;
+            s_stat[r] = 0;
+        } else {
+            // a later segment: the state the previous one left
+            const DecState d = state[c];
+            s_lower[r] = d.lower;
+            s_range[r] = d.range;
+            s_point[r] = d.point;
+            s_rpos[r] = d.rpos;
+            s_stat[r] = d.stat;
+        }
         s_wcnt[r] = cnt;
         s_woff[r] = woff;
         s_toff[r] = toff;
         s_len[r] = len;
-        s_stat[r] = 0;
         atomicMax(&s_maxlen, len);
     }
     __syncthreads();
     const int32_t maxlen = s_maxlen;
-    for (int32_t t = 0; t < maxlen; ++t) {
+    const int32_t t_stop = min(maxlen, t_end);
+    if (t_begin > 0 && t_begin < t_stop) {
+        // the context ring: the 64 tokens before t_begin, already written to
+        // `tokens` by the previous segment (segments end on multiples of 64,
+        // where the ring is flushed)
+        for (int i = threadIdx.x; i < R * WIN; i += THREADS) {
+            const int r = i / WIN;
+            const int32_t tp = t_begin - WIN + (i % WIN);
+            if (tp >= 0 && tp < s_len[r]) {
+                const int v = tokens[s_toff[r] + tp];
+                s_ring[r * WIN + (tp & (WIN - 1))] = (uint8_t)v;
+                if constexpr (PIPE) s_apos[r * WIN + (tp & (WIN - 1))] = (uint16_t)emb_off(v, 0);
+            }
+        }
+        __syncthreads();
+    }
+    for (int32_t t = t_begin; t < t_stop; ++t) {
         mlp_tile<PIPE, RT>(M, s_emb, s_act, s_par,
                            [&](int r, int p) {
                                const int q = r * WIN + ((t + p) & (WIN - 1));
@@ -416,7 +450,27 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         }
     }
     for (int r = threadIdx.x; r < R; r += THREADS)
-        if (c0 + r < n_chunks) status[c0 + r] = s_stat[r];
+        if (c0 + r < n_chunks) {
+            status[c0 + r] = s_stat[r];
+            if (t_stop < maxlen)
+                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], s_stat[r]};
+        }
+}
+
+// max(0, lengths[0 .. n-1]) -> out[0]; one workgroup of 1024 threads
+__global__ __launch_bounds__(1024) void k_max_len(const int32_t *__restrict__ lengths, int64_t n,
+                                                  int32_t *__restrict__ out) {
+    __shared__ int32_t s_m[1024 / 64];
+    int32_t mx = 0;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) mx = max(mx, lengths[i]);
+    mx = wave_max_i32(mx);
+    if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t r = 0;
+        for (int k = 0; k < 1024 / 64; ++k) r = max(r, s_m[k]);
+        out[0] = r;
+    }
 }
 
 // ---- word compaction -----------------------------------------------------
@@ -630,6 +684,12 @@ struct sc_model {
     int n_cu = 0;
     ModelDev dev{};
     std::vector<void *> allocs;
+    // decode: coder state carried between step segments (grown on demand),
+    // and the longest chunk length, computed on the device
+    mutable void *dec_state = nullptr;
+    mutable int64_t dec_state_chunks = 0;
+    mutable int32_t *len_max_dev = nullptr;
+    mutable int32_t *len_max_host = nullptr;   // pinned
 };
 
 namespace {
@@ -705,7 +765,7 @@ hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 // tiles per workgroup (MI355X, 512-token chunks, lossless model; us x 10 per
 // step; rt <= 4 runs the pipelined core).  Per row tile rt = 3 is cheapest
 // (41.4 us), rt = 1 the dearest (64.4 us).
-constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 644, 888, 1241, 1680, 2211, 2622};
+constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 644, 888, 1241, 1680, 2211};
 
 // Split `units` row tiles per CU into launch sizes of least summed step cost
 // (largest first, so that they take the longest chunks).
@@ -728,11 +788,18 @@ std::vector<int> dec_plan(int64_t units) {
 template <int RT>
 void dec_launch(const sc_model *m, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                 const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
-                int32_t *st) {
+                int32_t *st, DecState *state, int32_t t_begin, int32_t t_end) {
     auto *kern = m->dev.pipe && RT <= 4 ? k_decompress<RT, (RT <= 4)> : k_decompress<RT, false>;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, s, m->dev, words, woff, wcnt, len, count, tokens, toff,
-                       st);
+                       st, state, t_begin, t_end);
 }
+
+// Decode steps per launch.  Within one long launch the workgroups of an XCD
+// drift apart (after ~1000 steps by more than the L2 can bridge, and each
+// XCD then fetches the 6.2 MB model ~4 times per step from the memory side);
+// launches of 256 steps start them together again, so that one fetch serves
+// all of them (memory-side traffic of a c3 decode: 530 -> 215 GB).
+constexpr int DEC_SEG_STEPS = 256;
 
 }  // namespace
 
@@ -854,6 +921,9 @@ int sc_model_destroy(sc_model *m) {
     if (!m) return SC_OK;
     DeviceGuard guard(m->device);
     for (void *p : m->allocs) (void)hipFree(p);
+    if (m->dec_state) (void)hipFree(m->dec_state);
+    if (m->len_max_dev) (void)hipFree(m->len_max_dev);
+    if (m->len_max_host) (void)hipHostFree(m->len_max_host);
     delete m;
     return SC_OK;
 }
@@ -1022,6 +1092,32 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
         for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, DEC_RT_MAX))
             plan.push_back((int)std::min<int64_t>(u, DEC_RT_MAX));
     }
+    // step segments (SC_HIP_DEC_SEG overrides the length, 0 = one launch per
+    // group): the longest chunk bounds the segments of every group
+    const char *seg_env = getenv("SC_HIP_DEC_SEG");
+    int64_t seg = seg_env ? std::max(0, atoi(seg_env)) : DEC_SEG_STEPS;
+    seg = (seg + WIN - 1) / WIN * WIN;   // segments end where the token ring is flushed
+    int64_t maxlen = 0;
+    DecState *state = nullptr;
+    if (seg > 0) {
+        if (m->dec_state_chunks < n_chunks) {
+            if (m->dec_state) SC_HIP(hipFree(m->dec_state), "hipFree");
+            m->dec_state = nullptr;
+            m->dec_state_chunks = 0;
+            SC_HIP(hipMalloc(&m->dec_state, (size_t)n_chunks * sizeof(DecState)), "hipMalloc");
+            m->dec_state_chunks = n_chunks;
+        }
+        if (!m->len_max_dev) SC_HIP(hipMalloc((void **)&m->len_max_dev, sizeof(int32_t)), "hipMalloc");
+        if (!m->len_max_host) SC_HIP(hipHostMalloc((void **)&m->len_max_host, sizeof(int32_t)), "hipHostMalloc");
+        hipLaunchKernelGGL(k_max_len, dim3(1), dim3(1024), 0, s, lengths, n_chunks, m->len_max_dev);
+        int rc = check_launch("k_max_len");
+        if (rc) return rc;
+        SC_HIP(hipMemcpyAsync(m->len_max_host, m->len_max_dev, sizeof(int32_t), hipMemcpyDeviceToHost, s),
+               "hipMemcpyAsync");
+        SC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+        maxlen = *m->len_max_host;
+        state = (DecState *)m->dec_state;
+    }
     int64_t start = 0;
     size_t step = 0;
     while (start < n_chunks) {
@@ -1041,21 +1137,24 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
         const int64_t *woff = word_off + start, *toff = tok_off + start;
         const int32_t *wcnt = word_cnt + start, *len = lengths + start;
         int32_t *st = status + start;
-        switch (rt) {
+        DecState *ds = state ? state + start : nullptr;
+        for (int64_t tb = 0; tb == 0 || (seg > 0 && tb < maxlen); tb += (seg > 0 ? seg : INT32_MAX)) {
+            const int32_t t0 = (int32_t)tb, t1 = seg > 0 ? (int32_t)std::min<int64_t>(INT32_MAX, tb + seg) : INT32_MAX;
+            switch (rt) {
 #define SC_DEC_CASE(N)                                                                                        \
     case N:                                                                                                   \
-        dec_launch<N>(m, grid, s, wds, woff, wcnt, len, count, tokens, toff, st);                             \
+        dec_launch<N>(m, grid, s, wds, woff, wcnt, len, count, tokens, toff, st, ds, t0, t1);                 \
         break;
-            SC_DEC_CASE(1)
-            SC_DEC_CASE(2)
-            SC_DEC_CASE(3)
-            SC_DEC_CASE(4)
-            SC_DEC_CASE(5)
-            SC_DEC_CASE(6)
+                SC_DEC_CASE(1)
+                SC_DEC_CASE(2)
+                SC_DEC_CASE(3)
+                SC_DEC_CASE(4)
+                SC_DEC_CASE(5)
 #undef SC_DEC_CASE
+            }
+            const int rc = check_launch("k_decompress");
+            if (rc) return rc;
         }
-        const int rc = check_launch("k_decompress");
-        if (rc) return rc;
         start += count;
     }
     return SC_OK;
