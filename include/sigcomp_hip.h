@@ -196,15 +196,17 @@ int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t 
  * tile of chunks and runs the autoregressive loop for them (MLP step, fused
  * frequency step and decoder step per token, context kept on chip), in
  * launches of 256 steps (the coder state of each chunk is carried between
- * them in a device buffer the model keeps and grows on demand; the longest
- * chunk length is read back once per call, so the call waits for the work
- * already queued on `stream`).  Calls on one model must not overlap (issue
+ * them in a device buffer the model keeps and grows on demand; four chunk
+ * length statistics are read back once per call for the launch plan, so the
+ * call waits for the work already queued on `stream`).  Calls on one model
+ * must not overlap (issue
  * them on one stream).  Chunk c: word_cnt[c] words at words + word_off[c] ->
  * lengths[c] tokens at tokens + tok_off[c]; status[c] is written
  * (SC_STATUS_INVALID_STREAM on a corrupt stream, whose tokens are then
  * unspecified).  All arrays device.  Chunks sorted by descending length (as
  * QuantMLPCompression passes them) give the shortest schedule: the shortest
- * chunks then land in the final, partial launch.  Replaces
+ * chunks are then left over after the full waves of workgroups and follow
+ * the shortest chunks of the last full wave in the same rows.  Replaces
  * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
  * (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */

@@ -271,11 +271,22 @@ __global__ __launch_bounds__(256) void k_encode_pairs(const uint2 *__restrict__ 
 // windows (kept as 64-token rings in LDS), the fused frequency step and one
 // decoder step per chunk; the decoded token is appended to the ring.  Chunks
 // are independent, so workgroups never synchronise with each other.
-// Coder state of one chunk between the step segments of a decode.
+// Coder state of one row between the step segments of a decode: the state
+// of its current chunk, which of its chunks that is and the step it started.
 struct DecState {
     uint64_t lower, range, point;
-    int32_t rpos, stat;
+    int32_t rpos, stat, cur, start;
 };
+
+// CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474): the point is the
+// first two words, big-endian combined (one word -> w0 << 32)
+__device__ __forceinline__ uint64_t dec_init_point(const uint32_t *w, int cnt, int &take) {
+    uint64_t point = 0;
+    take = cnt < 2 ? cnt : 2;
+    for (int i = 0; i < take; ++i) point = (point << 32) | w[i];
+    if (cnt == 1) point <<= 32;
+    return point;
+}
 
 template <int RT, bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
@@ -286,7 +297,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                                            const int64_t *__restrict__ tok_off,
                                                            int32_t *__restrict__ status,
                                                            DecState *__restrict__ state, int32_t t_begin,
-                                                           int32_t t_end) {
+                                                           int32_t t_end, int64_t n_second) {
+    // Rows n_chunks - n_second .. n_chunks - 1 each decode a second chunk
+    // after their first one ends: row c continues with chunk
+    // 2 * n_chunks - 1 - c (the n_second chunks after the launch's own, in
+    // reverse order, so that with chunks sorted longest first the longest
+    // second chunk follows the shortest first chunk).
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
     static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
@@ -302,34 +318,44 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
     __shared__ int64_t s_woff[R], s_toff[R];
     __shared__ int32_t s_rpos[R], s_wcnt[R], s_len[R], s_stat[R];
+    // which chunk of the row is current (bit 0: the second one; bit 1: the
+    // row has a second chunk) and the step at which it started
+    __shared__ int32_t s_cur[R], s_start[R];
     __shared__ int32_t s_maxlen;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     const int64_t c0 = (int64_t)blockIdx.x * R;
-    load_emb_lds(M.emb, s_emb);
-    load_lut_lds(M.lut, s_lut);
-    mlp_tile_init<PIPE>(M, s_par, wave, lane);
     if (threadIdx.x == 0) s_maxlen = 0;
     __syncthreads();
     for (int r = threadIdx.x; r < R; r += THREADS) {
         const int64_t c = c0 + r;
+        const bool in = c < n_chunks;
+        // (the plain core's token ring cannot hold the start-of-sequence token)
+        const bool paired = PIPE && in && c >= n_chunks - n_second;
+        const int32_t len1 = in ? lengths[c] : 0;
+        const int32_t len2 = paired ? lengths[2 * n_chunks - 1 - c] : 0;
+        int32_t cur = 0, start = 0;
+        if (t_begin > 0 && in) {
+            cur = state[c].cur;
+            start = state[c].start;
+        } else if (paired && len1 <= 0) {
+            status[c] = 0;   // an empty first chunk: the second one starts at once
+            cur = 1;
+        }
+        const int64_t cc = cur ? 2 * n_chunks - 1 - c : c;
         int32_t len = 0, cnt = 0;
         int64_t woff = 0, toff = 0;
-        if (c < n_chunks) {
-            len = lengths[c];
-            cnt = word_cnt[c];
-            woff = word_off[c];
-            toff = tok_off[c];
+        if (in) {
+            len = lengths[cc];
+            cnt = word_cnt[cc];
+            woff = word_off[cc];
+            toff = tok_off[cc];
         }
-        if (t_begin == 0 || c >= n_chunks) {
-            // CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474)
-            uint64_t point = 0;
-            const int take = cnt < 2 ? cnt : 2;
-            for (int i = 0; i < take; ++i) point = (point << 32) | words[woff + i];
-            if (cnt == 1) point <<= 32;
+        if (t_begin == 0 || !in) {
+            int take;
+            s_point[r] = dec_init_point(words + woff, cnt, take);
             s_lower[r] = 0ull;
             s_range[r] = ~0ull;
-            s_point[r] = point;
             s_rpos[r] = take;
             s_stat[r] = 0;
         } else {
@@ -345,20 +371,30 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         s_woff[r] = woff;
         s_toff[r] = toff;
         s_len[r] = len;
-        atomicMax(&s_maxlen, len);
+        s_cur[r] = cur | (paired ? 2 : 0);   // bit 1: the row has a second chunk
+        s_start[r] = start;
+        atomicMax(&s_maxlen, max(len1, 0) + max(len2, 0));
     }
     __syncthreads();
     const int32_t maxlen = s_maxlen;
     const int32_t t_stop = min(maxlen, t_end);
-    if (t_begin > 0 && t_begin < t_stop) {
+    // a later segment past this workgroup's longest row: an earlier one
+    // finished its chunks and wrote their status (it saved no state)
+    if (t_begin > 0 && t_begin >= t_stop) return;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<PIPE>(M, s_par, wave, lane);
+    __syncthreads();
+    if (t_begin > 0) {
         // the context ring: the 64 tokens before t_begin, already written to
         // `tokens` by the previous segment (segments end on multiples of 64,
         // where the ring is flushed)
         for (int i = threadIdx.x; i < R * WIN; i += THREADS) {
             const int r = i / WIN;
-            const int32_t tp = t_begin - WIN + (i % WIN);
-            if (tp >= 0 && tp < s_len[r]) {
-                const int v = tokens[s_toff[r] + tp];
+            const int32_t tp = t_begin - WIN + (i % WIN), rs = tp - s_start[r];
+            if (tp >= 0 && rs < s_len[r]) {
+                // steps before the current chunk started are its start-of-sequence context
+                const int v = rs >= 0 ? (int)tokens[s_toff[r] + rs] : SOS;
                 s_ring[r * WIN + (tp & (WIN - 1))] = (uint8_t)v;
                 if constexpr (PIPE) s_apos[r * WIN + (tp & (WIN - 1))] = (uint16_t)emb_off(v, 0);
             }
@@ -388,13 +424,15 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
             uint64_t lower[EPI_N], range[EPI_N], point[EPI_N];
             int32_t rpos[EPI_N];
             uint32_t wnext[EPI_N];
-            bool active[EPI_N];
+            bool active[EPI_N], last1[EPI_N];
             v4i raw[EPI_N];
 #pragma unroll
             for (int n = 0; n < EPI_N; ++n) {
                 const int r = (gi + n * WAVES) * 4 + q4;
                 rr[n] = r;
-                active[n] = t < s_len[r] && s_stat[r] == 0;
+                const int32_t rs = t - s_start[r], len = s_len[r];
+                active[n] = rs < len && s_stat[r] == 0;
+                last1[n] = s_cur[r] == 2 && rs == len - 1;   // the row's first chunk ends with this step
                 lower[n] = s_lower[r];
                 range[n] = s_range[r];
                 point[n] = s_point[r];
@@ -437,6 +475,37 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                     if constexpr (PIPE) s_apos[r * WIN + (t & (WIN - 1))] = (uint16_t)emb_off(owner * 16 + u, 0);
                 }
                 if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
+                if (last1[n]) {
+                    // write out the first chunk's last tokens, then start the
+                    // second chunk from the next step with a start-of-sequence
+                    // context
+                    slot_sync();
+                    const int64_t c = c0 + r;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - s_start[r];
+                        if (pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
+                        if constexpr (PIPE) s_apos[r * WIN + 4 * u + k] = (uint16_t)emb_off(SOS, 0);
+                    }
+                    if (u == 0) {
+                        status[c] = s_stat[r];
+                        const int64_t c2 = 2 * n_chunks - 1 - c;
+                        const int32_t cnt = word_cnt[c2];
+                        const int64_t woff = word_off[c2];
+                        int take;
+                        s_point[r] = dec_init_point(words + woff, cnt, take);
+                        s_lower[r] = 0ull;
+                        s_range[r] = ~0ull;
+                        s_rpos[r] = take;
+                        s_stat[r] = 0;
+                        s_wcnt[r] = cnt;
+                        s_woff[r] = woff;
+                        s_toff[r] = tok_off[c2];
+                        s_len[r] = lengths[c2];
+                        s_cur[r] = 3;
+                        s_start[r] = t + 1;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -445,31 +514,50 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         // run instead of a byte per step
         if ((t & (WIN - 1)) == WIN - 1 || t == maxlen - 1) {
             const int32_t p = (t & ~(WIN - 1)) + lane;
-            for (int r = wave; r < R; r += WAVES)
-                if (p <= t && p < s_len[r]) tokens[s_toff[r] + p] = s_ring[r * WIN + lane];
+            for (int r = wave; r < R; r += WAVES) {
+                const int32_t rs = p - s_start[r];
+                if (p <= t && rs >= 0 && rs < s_len[r]) tokens[s_toff[r] + rs] = s_ring[r * WIN + lane];
+            }
         }
     }
     for (int r = threadIdx.x; r < R; r += THREADS)
         if (c0 + r < n_chunks) {
-            status[c0 + r] = s_stat[r];
+            const int64_t c = c0 + r;
+            const int cur = s_cur[r] & 1;
+            status[cur ? 2 * n_chunks - 1 - c : c] = s_stat[r];
             if (t_stop < maxlen)
-                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], s_stat[r]};
+                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], s_stat[r], cur, s_start[r]};
         }
 }
 
-// max(0, lengths[0 .. n-1]) -> out[0]; one workgroup of 1024 threads
-__global__ __launch_bounds__(1024) void k_max_len(const int32_t *__restrict__ lengths, int64_t n,
-                                                  int32_t *__restrict__ out) {
-    __shared__ int32_t s_m[1024 / 64];
-    int32_t mx = 0;
-    for (int64_t i = threadIdx.x; i < n; i += 1024) mx = max(mx, lengths[i]);
-    mx = wave_max_i32(mx);
-    if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = mx;
+// Length statistics for the decode plan, each max(0, ...), one workgroup of
+// 1024 threads.  With the last full-wave launch holding chunks g0 .. g0+G-1
+// and the `left` chunks after it: out[0] = the longest chunk, out[1] = the
+// longest pair (row g0+G-left+i of that launch followed by chunk
+// g0+G+left-1-i), out[2] = the longest chunk of that launch, out[3] = the
+// longest leftover chunk.
+__global__ __launch_bounds__(1024) void k_dec_lengths(const int32_t *__restrict__ lengths, int64_t n, int64_t g0,
+                                                      int64_t G, int64_t left, int32_t *__restrict__ out) {
+    __shared__ int32_t s_m[4][1024 / 64];
+    int32_t m[4] = {0, 0, 0, 0};
+    for (int64_t i = threadIdx.x; i < n; i += 1024) {
+        const int32_t l = max(lengths[i], 0);
+        m[0] = max(m[0], l);
+        if (i >= g0 && i < g0 + G) m[2] = max(m[2], l);
+        if (i >= g0 + G && i < g0 + G + left) m[3] = max(m[3], l);
+    }
+    for (int64_t i = threadIdx.x; i < left; i += 1024)
+        m[1] = max(m[1], max(lengths[g0 + G - left + i], 0) + max(lengths[g0 + G + left - 1 - i], 0));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        m[k] = wave_max_i32(m[k]);
+        if ((threadIdx.x & 63) == 0) s_m[k][threadIdx.x >> 6] = m[k];
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 4) {
         int32_t r = 0;
-        for (int k = 0; k < 1024 / 64; ++k) r = max(r, s_m[k]);
-        out[0] = r;
+        for (int k = 0; k < 1024 / 64; ++k) r = max(r, s_m[threadIdx.x][k]);
+        out[threadIdx.x] = r;
     }
 }
 
@@ -688,8 +776,8 @@ struct sc_model {
     // and the longest chunk length, computed on the device
     mutable void *dec_state = nullptr;
     mutable int64_t dec_state_chunks = 0;
-    mutable int32_t *len_max_dev = nullptr;
-    mutable int32_t *len_max_host = nullptr;   // pinned
+    mutable int32_t *len_stat_dev = nullptr;    // k_dec_lengths' 4 results
+    mutable int32_t *len_stat_host = nullptr;   // pinned
 };
 
 namespace {
@@ -788,10 +876,10 @@ std::vector<int> dec_plan(int64_t units) {
 template <int RT>
 void dec_launch(const sc_model *m, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                 const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
-                int32_t *st, DecState *state, int32_t t_begin, int32_t t_end) {
+                int32_t *st, DecState *state, int32_t t_begin, int32_t t_end, int64_t n_second) {
     auto *kern = m->dev.pipe && RT <= 4 ? k_decompress<RT, (RT <= 4)> : k_decompress<RT, false>;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, s, m->dev, words, woff, wcnt, len, count, tokens, toff,
-                       st, state, t_begin, t_end);
+                       st, state, t_begin, t_end, n_second);
 }
 
 // Decode steps per launch.  Within one long launch the workgroups of an XCD
@@ -922,8 +1010,8 @@ int sc_model_destroy(sc_model *m) {
     DeviceGuard guard(m->device);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->dec_state) (void)hipFree(m->dec_state);
-    if (m->len_max_dev) (void)hipFree(m->len_max_dev);
-    if (m->len_max_host) (void)hipHostFree(m->len_max_host);
+    if (m->len_stat_dev) (void)hipFree(m->len_stat_dev);
+    if (m->len_stat_host) (void)hipHostFree(m->len_stat_host);
     delete m;
     return SC_OK;
 }
@@ -1078,10 +1166,12 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     // full wave of n_cu workgroups.  The chunks of the full waves make
     // `units` row tiles per CU; with the pipelined core they are split into
     // launches by dec_plan (measured step costs), otherwise taken greedily
-    // at the largest rt.  The chunks left over (fewer than 32*n_cu) go to a
-    // final launch of rt = 1 workgroups.  With chunks sorted longest first
-    // the largest tiles get the longest chunks and the leftover launch the
-    // shortest ones.
+    // at the largest rt.  The chunks left over (fewer than 32*n_cu) either
+    // follow the last rows of the last full-wave launch in the same rows
+    // (pairing, pipelined core) or go to a final launch of rt = 1
+    // workgroups, whichever the step costs say is cheaper.  With chunks
+    // sorted longest first the largest tiles get the longest chunks and the
+    // leftover chunks are the shortest ones.
     const int64_t cu = m->n_cu;
     const int64_t units = n_chunks / (32 * cu);
     std::vector<int> plan;
@@ -1092,12 +1182,41 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
         for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, DEC_RT_MAX))
             plan.push_back((int)std::min<int64_t>(u, DEC_RT_MAX));
     }
+    const int64_t left = n_chunks - units * 32 * cu;
+    const int rt_last = plan.empty() ? 0 : plan.back();
+    const int64_t g_count = (int64_t)rt_last * 32 * cu, g0 = units * 32 * cu - g_count;
+    const char *pair_env = getenv("SC_HIP_DEC_PAIR");   // "0": never pair (comparisons)
+    const bool can_pair = m->dev.pipe && rt_last >= 1 && rt_last <= 4 && left > 0 && left <= g_count &&
+                          !(pair_env && std::strcmp(pair_env, "0") == 0);
     // step segments (SC_HIP_DEC_SEG overrides the length, 0 = one launch per
-    // group): the longest chunk bounds the segments of every group
+    // group): the longest row bounds the segments of every group
     const char *seg_env = getenv("SC_HIP_DEC_SEG");
     int64_t seg = seg_env ? std::max(0, atoi(seg_env)) : DEC_SEG_STEPS;
     seg = (seg + WIN - 1) / WIN * WIN;   // segments end where the token ring is flushed
-    int64_t maxlen = 0;
+    if (!m->len_stat_dev) SC_HIP(hipMalloc((void **)&m->len_stat_dev, 4 * sizeof(int32_t)), "hipMalloc");
+    if (!m->len_stat_host) SC_HIP(hipHostMalloc((void **)&m->len_stat_host, 4 * sizeof(int32_t)), "hipHostMalloc");
+    hipLaunchKernelGGL(k_dec_lengths, dim3(1), dim3(1024), 0, s, lengths, n_chunks, g0, g_count,
+                       can_pair ? left : (int64_t)0, m->len_stat_dev);
+    int rc = check_launch("k_dec_lengths");
+    if (rc) return rc;
+    SC_HIP(hipMemcpyAsync(m->len_stat_host, m->len_stat_dev, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, s),
+           "hipMemcpyAsync");
+    SC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const int32_t len_max = m->len_stat_host[0], pair_max = m->len_stat_host[1];
+    const int32_t group_max = m->len_stat_host[2], left_max = m->len_stat_host[3];
+    // pairing lengthens the last full-wave launch by the steps its longest
+    // pair exceeds its longest chunk; the rt = 1 launch costs the longest
+    // leftover chunk's steps
+    const bool pair = can_pair && (int64_t)std::max(0, pair_max - group_max) * DEC_STEP_COST[rt_last] <
+                                      (int64_t)left_max * DEC_STEP_COST[1];
+    const int64_t maxlen = std::max(len_max, pair ? pair_max : 0);
+    if (const char *log = getenv("SC_HIP_DEC_LOG"); log && std::strcmp(log, "1") == 0) {
+        std::string rts;
+        for (int rt : plan) rts += (rts.empty() ? "" : ",") + std::to_string(rt);
+        std::fprintf(stderr, "sc_decompress_chunks: chunks %lld cu %lld plan [%s] leftover %lld %s steps %lld seg %lld\n",
+                     (long long)n_chunks, (long long)cu, rts.c_str(), (long long)left,
+                     left == 0 ? "none" : pair ? "paired" : "launch", (long long)maxlen, (long long)seg);
+    }
     DecState *state = nullptr;
     if (seg > 0) {
         if (m->dec_state_chunks < n_chunks) {
@@ -1107,31 +1226,23 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
             SC_HIP(hipMalloc(&m->dec_state, (size_t)n_chunks * sizeof(DecState)), "hipMalloc");
             m->dec_state_chunks = n_chunks;
         }
-        if (!m->len_max_dev) SC_HIP(hipMalloc((void **)&m->len_max_dev, sizeof(int32_t)), "hipMalloc");
-        if (!m->len_max_host) SC_HIP(hipHostMalloc((void **)&m->len_max_host, sizeof(int32_t)), "hipHostMalloc");
-        hipLaunchKernelGGL(k_max_len, dim3(1), dim3(1024), 0, s, lengths, n_chunks, m->len_max_dev);
-        int rc = check_launch("k_max_len");
-        if (rc) return rc;
-        SC_HIP(hipMemcpyAsync(m->len_max_host, m->len_max_dev, sizeof(int32_t), hipMemcpyDeviceToHost, s),
-               "hipMemcpyAsync");
-        SC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
-        maxlen = *m->len_max_host;
         state = (DecState *)m->dec_state;
     }
     int64_t start = 0;
     size_t step = 0;
     while (start < n_chunks) {
-        const int64_t left = n_chunks - start;
-        int64_t rt, count;
+        const int64_t rest = n_chunks - start;
+        int64_t rt, count, n_second = 0;
         unsigned grid;
         if (step < plan.size()) {
             rt = plan[step++];
             count = cu * 32 * rt;
             grid = (unsigned)cu;
+            if (pair && step == plan.size()) n_second = left;
         } else {
             rt = 1;
-            count = left;
-            grid = (unsigned)((left + 31) / 32);
+            count = rest;
+            grid = (unsigned)((rest + 31) / 32);
         }
         const uint32_t *wds = words;
         const int64_t *woff = word_off + start, *toff = tok_off + start;
@@ -1143,7 +1254,7 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
             switch (rt) {
 #define SC_DEC_CASE(N)                                                                                        \
     case N:                                                                                                   \
-        dec_launch<N>(m, grid, s, wds, woff, wcnt, len, count, tokens, toff, st, ds, t0, t1);                 \
+        dec_launch<N>(m, grid, s, wds, woff, wcnt, len, count, tokens, toff, st, ds, t0, t1, n_second);       \
         break;
                 SC_DEC_CASE(1)
                 SC_DEC_CASE(2)
@@ -1152,10 +1263,10 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
                 SC_DEC_CASE(5)
 #undef SC_DEC_CASE
             }
-            const int rc = check_launch("k_decompress");
+            rc = check_launch("k_decompress");
             if (rc) return rc;
         }
-        start += count;
+        start += count + n_second;
     }
     return SC_OK;
 }

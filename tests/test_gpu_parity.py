@@ -290,6 +290,111 @@ def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, units, extra
     assert [words[woff[i]:woff[i] + wcnt[i]].tobytes() for i in sample] == ref
 
 
+def _decode_direct(codec, words, woff, wcnt, lengths):
+    """sc_decompress_chunks on the chunks in the order given (the C ABI does
+    not sort) -> (tokens of all chunks in chunk order, per-chunk status).
+    Status starts at -1 so that a chunk whose status is never written shows."""
+    from sigcomp_amd import _hip
+    n = len(lengths)
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
+    n_tok = int(lengths.sum())
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_words, t_woff, t_cnt = d(words.view(np.int32)), d(woff.astype(np.int64)), d(wcnt.astype(np.int32))
+    t_len, t_toff = d(lengths.astype(np.int32)), d(tok_off)
+    tokens = torch.zeros(max(n_tok, 1), dtype=torch.uint8, device="cuda")
+    status = torch.full((n,), -1, dtype=torch.int32, device="cuda")
+    _hip.check(_hip.lib().sc_decompress_chunks(
+        codec.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt), _hip.ptr(t_len), n,
+        _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status), _hip.stream_ptr()))
+    torch.cuda.synchronize()
+    return tokens.cpu().numpy()[:n_tok], status.cpu().numpy(), tok_off
+
+
+def _set_dec_env(monkeypatch, seg):
+    monkeypatch.setenv("SC_HIP_DEC_LOG", "1")
+    if seg is None:
+        monkeypatch.delenv("SC_HIP_DEC_SEG", raising=False)
+    else:
+        monkeypatch.setenv("SC_HIP_DEC_SEG", str(seg))
+
+
+@pytest.mark.parametrize("seg", [None, 64, 0])
+def test_decompress_pairs_leftover_chunks(codecs, capfd, monkeypatch, seg):
+    """The chunks left over after the full waves (here 300, the shortest)
+    are decoded by the last full-wave launch's shortest rows after their own
+    chunk ends; default 256-step segments, 64-step segments, one launch."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    G, L = 2 * 32 * n_cu, 300
+    rng = np.random.default_rng(31 + (seg or 0))
+    lengths = np.concatenate([rng.integers(900, 1201, G - L), rng.integers(1, 701, 2 * L)]).astype(np.int32)
+    rng.shuffle(lengths)
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    _set_dec_env(monkeypatch, seg)
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "leftover 300 paired" in log, log
+    assert np.array_equal(back, tokens)
+
+
+def test_decompress_rejects_pairing_of_long_leftovers(codecs, capfd, monkeypatch):
+    """Leftover chunks as long as the rest would stretch the last full-wave
+    launch (64-chunk workgroups) by more than a separate leftover launch
+    costs: no pairing."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    n = 2 * 32 * n_cu + 40
+    rng = np.random.default_rng(8)
+    lengths = rng.integers(550, 601, n).astype(np.int32)
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    _set_dec_env(monkeypatch, None)
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "leftover 40 launch" in log, log
+    assert np.array_equal(back, tokens)
+
+
+@pytest.mark.parametrize("seg", [None, 64])
+def test_decompress_paired_rows_status_and_edges(codecs, capfd, monkeypatch, seg):
+    """Pairing through the C ABI on unsorted chunks: first chunks that end on
+    64- and 256-step edges, an empty first chunk, and corrupt first and
+    second chunks.  Each corrupt chunk (and only it) reports an invalid
+    stream; the other chunk of its row still decodes."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    G, L = 32 * n_cu, 120
+    rng = np.random.default_rng(77 if seg is None else seg)
+    lengths = np.concatenate([rng.integers(800, 1001, G - L), rng.integers(100, 401, L),
+                              rng.integers(1, 301, L)]).astype(np.int32)
+    # rows G-L .. G-1 are the paired first chunks; row c's second is 2G-1-c
+    edge = [63, 64, 65, 127, 128, 255, 256, 257, 320, 383, 384, 385]
+    lengths[G - L:G - L + len(edge)] = edge
+    lengths[G - 1] = 0
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    bad = [G - L + 20, 2 * G - 1 - (G - L + 30), G - L + 6]   # a first, a second, an edge first chunk
+    words = np.concatenate([words, np.full(2, 0xFFFFFFFF, np.uint32)])
+    woff, wcnt = woff.copy(), wcnt.copy()
+    woff[bad], wcnt[bad] = len(words) - 2, 2
+    capfd.readouterr()
+    _set_dec_env(monkeypatch, seg)
+    back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert f"leftover {L} paired" in log, log
+    expect = np.zeros(len(lengths), np.int32)
+    expect[bad] = 2   # SC_STATUS_INVALID_STREAM
+    assert np.array_equal(status, expect)
+    for i in range(len(lengths)):
+        if i not in bad:
+            s = slice(tok_off[i], tok_off[i] + lengths[i])
+            assert np.array_equal(back[s], tokens[s]), i
+
+
 def test_mfma_burn_hook_computes_its_products():
     """The power-limit measurement hook (sc_mfma_burn_i8) really issues the
     MFMAs it is timed for: its accumulator sums equal the int8 matrix
