@@ -35,6 +35,15 @@ from .model_io import (DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MO
 _MIN_LAUNCH_CHUNKS = 1 << 16
 
 
+def _to_device(a, dev):
+    """Host array -> device tensor (read-only arrays, e.g. views of a bytes
+    object, are copied first: torch only wraps writable memory)."""
+    a = np.ascontiguousarray(a)
+    if not a.flags.writeable:
+        a = a.copy()
+    return torch.from_numpy(a).to(dev)
+
+
 class HipModel:
     """An ``IntModel`` uploaded to one GPU (owns the ``sc_model`` handle)."""
 
@@ -206,7 +215,7 @@ class QuantMLPCompression(ReadFramingMixin):
         word_off = np.zeros(n, dtype=np.int64)
         np.cumsum(cap[:-1], dtype=np.int64, out=word_off[1:])
         dev = self.hip.device
-        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev, non_blocking=False)
+        d = lambda a: _to_device(a, dev)
         t_tokens, t_tok_off, t_len = d(tokens), d(tok_off), d(lengths)
         t_word_off, t_cap = d(word_off), d(cap.astype(np.int32))
         words, cnt, status, ws = self._compress_buffers(n, n_tokens, int(cap.sum()))
@@ -303,7 +312,7 @@ class QuantMLPCompression(ReadFramingMixin):
         # length and stops at its own longest one
         order = np.argsort(-lengths, kind="stable")
         dev = self.hip.device
-        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        d = lambda a: _to_device(a, dev)
         t_words = d(words.view(np.int32))
         t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(lengths[order]), d(tok_off[order])
         tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)

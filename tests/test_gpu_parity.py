@@ -395,6 +395,30 @@ def test_decompress_paired_rows_status_and_edges(codecs, capfd, monkeypatch, seg
             assert np.array_equal(back[s], tokens[s]), i
 
 
+def test_decompress_status_survives_later_segments(codecs, monkeypatch):
+    """A corrupt chunk in a workgroup whose rows all end in the first 64-step
+    launch keeps its status through the later launches another workgroup's
+    long chunk needs (those launches find nothing left to do there)."""
+    rng = np.random.default_rng(4)
+    lengths = np.full(64, 10, np.int32)
+    lengths[0] = 300
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    words = np.concatenate([words, np.full(2, 0xFFFFFFFF, np.uint32)])
+    woff, wcnt = woff.copy(), wcnt.copy()
+    woff[40], wcnt[40] = len(words) - 2, 2
+    monkeypatch.setenv("SC_HIP_DEC_SEG", "64")
+    for _ in range(2):   # the second call starts from the first call's decode state buffer
+        back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths)
+        expect = np.zeros(64, np.int32)
+        expect[40] = 2
+        assert np.array_equal(status, expect)
+        keep = np.ones(len(back), bool)
+        keep[tok_off[40]:tok_off[40] + 10] = False
+        assert np.array_equal(back[keep], tokens[keep])
+
+
 def test_mfma_burn_hook_computes_its_products():
     """The power-limit measurement hook (sc_mfma_burn_i8) really issues the
     MFMAs it is timed for: its accumulator sums equal the int8 matrix
