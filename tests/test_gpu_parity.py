@@ -265,6 +265,39 @@ def test_plain_core_matches_oracle(oracle_mod, monkeypatch, which):
     assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
 
 
+@pytest.mark.parametrize("core", ["pipelined", "plain"])
+def test_fast_requant_clamp_bounds_match_oracle(oracle_mod, monkeypatch, core):
+    """Fast-path layers (every shift >= 32) whose per-channel shifts span
+    32..63: shift - 32 >= 24 (the pre-shift clamp bound held at INT32_MAX),
+    shifts that saturate most values at 127 and, on the output layer, at
+    -128, and shifts that leave 0 / -1."""
+    from sigcomp_amd.model_io import make_layer, random_int_model
+    from sigcomp_amd.quant_mlp_export import HipModel
+    import dataclasses
+    m = random_int_model(seed=13, per_channel=True)
+    rng = np.random.default_rng(13)
+    layers = list(m.layers)
+    for li in (2, len(layers) - 1):
+        L = layers[li]
+        shift = np.full(L.n, 36, np.int32)
+        for r, s in enumerate((32, 33, 56, 63, 55, 44)):
+            shift[r::7] = s
+        m0 = rng.integers(1 << 30, (1 << 31) - 1, L.n)
+        layers[li] = make_layer(L.weight, L.bias, m0, shift, L.relu)
+    model = dataclasses.replace(m, layers=layers)
+    if core == "plain":
+        monkeypatch.setenv("SC_HIP_PLAIN_CORE", "1")
+    hm = HipModel(model, torch.device("cuda:0"))
+    monkeypatch.delenv("SC_HIP_PLAIN_CORE", raising=False)
+    assert hm.pipelined == (core == "pipelined")
+    ctx = rng.integers(0, 257, (300, 64))
+    ctx[:40, :25] = 256
+    exp = oracle_mod.mlp_forward(oracle_mod.OracleModel(model), ctx)
+    assert (exp == 127).any() and (exp == -128).any() and (exp == -1).any()
+    got = hm.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
+    assert np.array_equal(got, exp)
+
+
 def test_pipelined_core_selected_for_bundled_models(codecs):
     assert codecs["lossless"].hip.pipelined and codecs["lossy"].hip.pipelined
 
