@@ -1,6 +1,6 @@
 """SigComp codec benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c2|ceiling|coder]
 
 Default workload (config c3+c4): 4,000 seeded synthetic R10.4.1-like reads
 (~80 M int16 samples), bundled lossless model, chunk_len 2048.  One step =
@@ -18,7 +18,9 @@ sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c2 = MLP
 microbenchmark (1,048,576 context rows -> int32 CDF tables); ceiling = the
 int8 MFMA rate the GPU sustains at its power limit (register-operand MFMA
 chains on every CU, random and zero operands), recorded in
-profiles/mfma_ceiling.txt and quoted beside the 5.0 POP/s spec peak.
+profiles/mfma_ceiling.txt and quoted beside the 5.0 POP/s spec peak;
+coder = the step-API coder kernels (logits -> CDF, encode step, decode
+step) timed as their own launches against HBM bandwidth.
 """
 
 from __future__ import annotations
@@ -370,6 +372,104 @@ def bench_ceiling(args):
             "frac_of_peak": round(res["random"] / PEAK_INT8_TOPS, 4)}
 
 
+# Algorithmic HBM bytes per stream and step of the coder step kernels
+# (device arrays as GpuRangeStepEncoder / GpuRangeDecoder keep them), words
+# excluded (added from the measured word count):
+#   k_logits_to_cdf: 256 B logits in, 257 x int64 CDF out
+#   k_encode_step:   logits 256, symbol 8, valid 8, status 4, state read and
+#                    written (lower 8, range 8, inverted 4, first 4, pos 4)
+#   k_decode_step:   logits 256, valid 8, status 4, state read (lower, range,
+#                    point, read_pos, end_pos: 40) and written (32), symbol 8
+CODER_BYTES = {"k_logits_to_cdf": 256 + 257 * 8, "k_encode_step": 256 + 8 + 8 + 4 + 2 * 28,
+               "k_decode_step": 256 + 8 + 4 + 40 + 32 + 8}
+
+
+def bench_coder(args):
+    """The reference's step-API coder kernels timed as
+    their own launches, HIP events on the launching stream: B streams of
+    synthetic int8 logits per step (normal, sd 20; the coded symbol is the
+    argmax of the logits plus uniform noise), `steps` steps, called through
+    the C ABI.  At B = 1,048,576 one step's logits (268 MB) exceed the 256 MB
+    MALL, so the launches stream from HBM; B = 20,480 (the reference's batch)
+    shows the launch-bound regime.  The decoder, fed the encoder's sealed
+    words, must return every coded symbol."""
+    import torch
+    from sigcomp_amd import _hip
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
+    from sigcomp_amd.model_io import load_int_model
+    dev = torch.device("cuda:0")
+    L = _hip.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lut = torch.from_numpy(load_int_model().exp_lut.astype(np.int64)).to(dev)
+    T = max(2, args.steps)
+    out = {}
+    for B in (args.rows, 20480):
+        g = torch.Generator(device=dev).manual_seed(5)
+        logits = [(torch.randn(B, 256, generator=g, device=dev) * 20).round().clamp(-128, 127).to(torch.int8)
+                  for _ in range(T)]
+        syms = [torch.argmax(lg.float() + torch.rand(B, 256, generator=g, device=dev) * 40, dim=1)
+                for lg in logits]
+        valid = torch.full((B,), T, dtype=torch.int64, device=dev)
+        cdf = torch.empty((B, 257), dtype=torch.int64, device=dev)
+        enc = GpuRangeStepEncoder(B, T + 32, device=dev)
+
+        def timed(fn):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for t in range(T):
+                _hip.check(fn(t))
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / 1e3 / T
+
+        p = _hip.ptr
+        # first launches load the kernels' code object: untimed, and at
+        # t = T every stream is inactive (no coder state changes)
+        scratch = torch.empty(B, dtype=torch.int64, device=dev)
+        _hip.check(L.sc_logits_to_cdf(p(logits[0]), B, p(lut), p(cdf), stream))
+        _hip.check(L.sc_encode_step(p(logits[0]), p(lut), p(syms[0]), p(valid), T, B, enc._state,
+                                    p(enc.output_words), enc.max_words, stream))
+        t_cdf = timed(lambda t: L.sc_logits_to_cdf(p(logits[t]), B, p(lut), p(cdf), stream))
+        t_enc = timed(lambda t: L.sc_encode_step(p(logits[t]), p(lut), p(syms[t]), p(valid), t, B, enc._state,
+                                                 p(enc.output_words), enc.max_words, stream))
+        words = enc.get_compressed()
+        wpt = sum(len(w) for w in words) / 4 / (B * T)     # words per stream-step, seal included
+        dec = GpuRangeDecoder(words, device=dev)
+        got = torch.empty((T, B), dtype=torch.int64, device=dev)
+        _hip.check(L.sc_decode_step(p(logits[0]), p(lut), p(valid), T, B, dec._state, p(dec.comp_words),
+                                    p(scratch), stream))
+        t_dec = timed(lambda t: L.sc_decode_step(p(logits[t]), p(lut), p(valid), t, B, dec._state,
+                                                 p(dec.comp_words), p(got[t]), stream))
+        dec.check()
+        if not all(torch.equal(got[t], syms[t]) for t in range(T)):
+            raise RuntimeError("coder round trip mismatch")
+        res = {}
+        for k, tk, extra in (("k_logits_to_cdf", t_cdf, 0.0), ("k_encode_step", t_enc, 4 * wpt),
+                             ("k_decode_step", t_dec, 4 * wpt)):
+            gbs = B * (CODER_BYTES[k] + extra) / tk / 1e9
+            res[k] = {"us_per_launch": round(tk * 1e6, 2), "gb_s": round(gbs, 1),
+                      "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                      "bytes_per_stream": round(CODER_BYTES[k] + extra, 2)}
+        res["words_per_stream_step"] = round(wpt, 4)
+        out[B] = res
+        log(f"[bench] coder B={B}: " + ", ".join(f"{k} {v['us_per_launch']} us {v['gb_s']} GB/s"
+                                                for k, v in res.items() if k.startswith("k_")))
+        del logits, syms, enc, dec, got, cdf, scratch
+    big = out[args.rows]
+    d = big["k_decode_step"]
+    return {"metric": "range-coder step kernels (logits->CDF, encode step, decode step), HBM GB/s",
+            "value": d["gb_s"], "unit": "GB/s (k_decode_step)", "n_gpus": 1, "steps": T, "warmup": 0,
+            "ms_per_step": round(d["us_per_launch"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+            "config": {"workload": f"coder: {args.rows} streams x {T} steps of synthetic int8 logits "
+                                   f"(and {20480} streams, the reference's batch)"},
+            "roofline": {"kernel": "k_decode_step", "bound": "hbm", "achieved": d["gb_s"], "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": d["frac_of_hbm"], "traffic": None,
+                         "algorithmic": f"{d['bytes_per_stream']} B per stream and step x {args.rows} streams"},
+            "kernels": {str(B): v for B, v in out.items()}}
+
+
 def power_capped_peak():
     """Sustained int8 MFMA rate with random operands, measured by
     `bench.py --config ceiling` and recorded in profiles/mfma_ceiling.txt."""
@@ -395,7 +495,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2", "ceiling"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2", "ceiling", "coder"])
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -411,6 +511,9 @@ def main():
         return
     if args.config == "ceiling":
         print(json.dumps(bench_ceiling(args)), flush=True)
+        return
+    if args.config == "coder":
+        print(json.dumps(bench_coder(args)), flush=True)
         return
     res, chunks, samples, cfg, gpu_out = bench_codec(args)
     if not args.no_cpu_baseline:

@@ -580,7 +580,10 @@ __global__ __launch_bounds__(256) void k_gather_words(const uint32_t *__restrict
 }
 
 // ---- step-API kernels (GpuRangeStepEncoder / GpuRangeDecoder) ------------
-// 256 threads = 16 rows per workgroup (four 16-lane rows per wavefront).
+// 256 threads = 16 rows per workgroup (four 16-lane rows per wavefront).  A
+// workgroup's rows are a short serial chain (LUT staging, loads, frequency
+// step, coder step), run by many workgroups per CU at once (few registers);
+// k_logits_to_cdf issues its logits load before the LUT staging barrier.
 
 __device__ __forceinline__ void stage_lut(const uint64_t *lut, double *s_lut) {
     load_lut_lds(lut, s_lut);
@@ -595,11 +598,12 @@ __global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict_
                                                        const uint64_t *__restrict__ lut,
                                                        int64_t *__restrict__ cdf) {
     __shared__ double s_lut[VOCAB];
-    stage_lut(lut, s_lut);
     const int u = threadIdx.x & 15;
     const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const v4i raw = global_logits16(logits, r, rows, u);
+    stage_lut(lut, s_lut);
     Freq16 fr;
-    row_frequencies16(global_logits16(logits, r, rows, u), s_lut, u, fr);
+    row_frequencies16(raw, s_lut, u, fr);
     if (r >= rows) return;
     int64_t *dst = cdf + r * (VOCAB + 1) + 16 * u;
     uint32_t c = fr.ex;

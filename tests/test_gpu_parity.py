@@ -148,6 +148,36 @@ def test_step_encoder_and_decoder_match_reference(int_models, name):
         assert np.all(got[b, valid[b]:] == 256)
 
 
+def test_step_api_many_streams(int_models, oracle_mod):
+    """More rows and streams than one pass of the launch's workgroups covers
+    (2048 x 32 rows per pass of the persistent row loop): 150,001 CDF rows
+    against the oracle, and 70,001 streams x 3 encode / decode steps whose
+    decoder returns every coded symbol, with a few streams inactive."""
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder, int8_logits_to_cdf
+    lut_np = int_models["lossless"].exp_lut
+    g = torch.Generator(device="cuda").manual_seed(3)
+    rows = (torch.randn(150001, 256, generator=g, device="cuda") * 20).round().clamp(-128, 127).to(torch.int8)
+    cdf = int8_logits_to_cdf(rows, lut_np).cpu().numpy()
+    sub = np.r_[0:300, 65530:65600, 149800:150001]
+    assert np.array_equal(cdf[sub], oracle_mod.logits_to_cdf(rows.cpu().numpy()[sub], lut_np))
+    B, T = 70001, 3
+    lut = torch.from_numpy(lut_np)
+    lg = [(torch.randn(B, 256, generator=g, device="cuda") * 20).round().clamp(-128, 127).to(torch.int8)
+          for _ in range(T)]
+    sy = [torch.randint(0, 256, (B,), generator=g, device="cuda") for _ in range(T)]
+    valid = torch.full((B,), T, dtype=torch.int64, device="cuda")
+    valid[::1000] = 1
+    enc = GpuRangeStepEncoder(B, T + 32, device="cuda")
+    for t in range(T):
+        enc.encode_step_int8(lg[t], lut, sy[t], valid, t)
+    dec = GpuRangeDecoder(enc.get_compressed(), device="cuda")
+    for t in range(T):
+        got = dec.decode_step_int8(lg[t], lut, valid, t).clone()
+        exp = torch.where(valid > t, sy[t], torch.full_like(sy[t], 256))
+        assert torch.equal(got, exp), t
+    dec.check()
+
+
 def test_step_decoder_flags_invalid_stream(int_models):
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
     bad = np.array([0xFFFFFFFF, 0xFFFFFFFF], np.uint32).tobytes()
