@@ -39,10 +39,9 @@ constexpr int EMB_BYTES = EMB_ROWS * EMB_STRIDE;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Requant parameters of one 32-output n-tile, 104 dwords: bias[32] (int32),
-// m0[32] (uint32), shift[32] (uint8, packed four per dword), hi[32] (int32;
-// fast-path layers: the pre-shift clamp bound of rq_byte).
-constexpr int PAR_DWORDS = 104;
+// Requant parameters of one 32-output n-tile, 72 dwords: bias[32] (int32),
+// m0[32] (uint32), shift[32] (uint8, packed four per dword).
+constexpr int PAR_DWORDS = 72;
 constexpr int PAR_LDS_DWORDS = 4 * PAR_DWORDS * 4;   // 4 waves x up to 4 n-tiles
 
 struct LayerDev {
@@ -147,41 +146,6 @@ __device__ __forceinline__ uint32_t requant_u8_fast(int acc, int bias, int m0, u
     const int biased = (int)((uint32_t)acc + (uint32_t)bias);
     const int s = __mulhi(biased, m0) >> shift32;
     return (uint32_t)(uint8_t)(int8_t)min(max(s, lo), 127);
-}
-
-// The fast path in four VALU instructions per value with the accumulator
-// read: x = hi32(a * m0) is clamped BEFORE the per-channel shift sh, to
-// [lo * 2**sh, 128 * 2**sh - 1] held inside the int32 range (hi from the
-// parameter block; lo = 0 with ReLU, else ~hi = -128 * 2**sh).
-// floor(x / 2**sh) is monotone in x, so this equals min(max(x >> sh, lo),
-// 127) of requant_u8_fast; the arithmetic shift then writes the byte
-// directly (rq_insert).
-template <bool RELU>
-__device__ __forceinline__ int rq_clamp(int a, int m0, int hi) {
-    const int x = __mulhi(a, m0);
-    // med3 = min(max(x, lo), hi) since lo <= hi (the compiler cannot know
-    // that of a loaded bound and would emit a max and a min)
-    int y;
-    if constexpr (RELU) asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y) : "v"(x), "v"(hi));
-    else asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(x), "v"(~hi), "v"(hi));
-    return y;
-}
-// byte E of `packed` = (y >> (byte E of shw)) & 0xff (SDWA destination and
-// source selects; byte 0 clears the other bytes)
-template <int E>
-__device__ __forceinline__ void rq_insert(uint32_t &packed, uint32_t shw, int y) {
-    if constexpr (E == 0)
-        asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
-            : "=v"(packed) : "v"(shw), "v"(y));
-    else if constexpr (E == 1)
-        asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:DWORD"
-            : "+v"(packed) : "v"(shw), "v"(y));
-    else if constexpr (E == 2)
-        asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2 src1_sel:DWORD"
-            : "+v"(packed) : "v"(shw), "v"(y));
-    else
-        asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3 src1_sel:DWORD"
-            : "+v"(packed) : "v"(shw), "v"(y));
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1, so
@@ -421,38 +385,33 @@ __device__ __forceinline__ void requant_pack_t(const v16i (&acc)[NTP][RT], const
 #pragma unroll
     for (int j = 0; j < NTP; ++j) {
         const uint32_t *pj = par + j * PAR_DWORDS;
-        v4i bb[4] = {}, mm[4], hh[4] = {};
-        uint32_t shw[4], sh[4][4];
+        v4i bb[4] = {}, mm[4];
+        uint32_t sh[4][4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int o = 8 * g + 4 * g2;
             if constexpr (BIAS) bb[g] = *(const v4i *)(pj + o);
             mm[g] = *(const v4i *)(pj + 32 + o);
-            if constexpr (FAST) hh[g] = *(const v4i *)(pj + 72 + o);
-            shw[g] = pj[64 + (o >> 2)];
+            const uint32_t ss = pj[64 + (o >> 2)];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sh[g][e] = (shw[g] >> (8 * e)) & 63u;
+            for (int e = 0; e < 4; ++e) sh[g][e] = (ss >> (8 * e)) & 63u;
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
 #pragma unroll
             for (int i = 0; i < RT; ++i) {
                 uint32_t packed = 0;
-                static_for<4>([&](auto ec) __attribute__((always_inline)) {
-                    constexpr int e = decltype(ec)::value;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
                     // read the accumulator out of its AGPR here, one at a
                     // time (otherwise every accumulator is copied to VGPRs
                     // at the end of the k loop, which spills)
                     int a;
                     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[j][i][4 * g + e]));
-                    if constexpr (FAST) {
-                        rq_insert<e>(packed, shw[g], rq_clamp<RELU>((int)((uint32_t)a + (uint32_t)bb[g][e]), mm[g][e],
-                                                                   hh[g][e]));
-                    } else {
-                        const uint32_t q = requant_u8(a, bb[g][e], (uint32_t)mm[g][e], sh[g][e], lo);
-                        packed |= q << (8 * e);
-                    }
-                });
+                    const uint32_t q = FAST ? requant_u8_fast(a, bb[g][e], mm[g][e], sh[g][e], lo)
+                                            : requant_u8(a, bb[g][e], (uint32_t)mm[g][e], sh[g][e], lo);
+                    packed |= q << (8 * e);
+                }
                 // materialise the packed word here: without this the compiler
                 // sinks the requantisation below the next pass's GEMM and keeps
                 // every accumulator and parameter alive across it (spills)

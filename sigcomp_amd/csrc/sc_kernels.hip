@@ -958,10 +958,9 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         if (rc) break;
         // Requant constants.  m0 == 2**31 is rewritten as (2**30, shift - 1)
         // (the same product); layers whose every m0 < 2**31 and shift >= 32
-        // take the 32-bit high-product path (requant_u8_fast / rq_byte),
-        // with shift - 32 stored and hi = 128 * 2**(shift - 32) - 1, held at
-        // INT32_MAX.  Packed per 32-output n-tile: bias[32], m0[32],
-        // shift[32] (bytes), hi[32], PAR_DWORDS dwords per n-tile.
+        // take the 32-bit high-product path (requant_u8_fast), with
+        // shift - 32 stored.  Packed per 32-output n-tile: bias[32], m0[32],
+        // shift[32] (bytes), PAR_DWORDS dwords per n-tile.
         std::vector<uint32_t> m0(L.n);
         std::vector<uint8_t> sh(L.n);
         bool fast = true;
@@ -987,7 +986,6 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
                 blk[x] = (uint32_t)L.bias[j];
                 blk[32 + x] = m0[j];
                 blk[64 + x / 4] |= (uint32_t)sh[j] << (8 * (x % 4));
-                blk[72 + x] = fast ? (sh[j] >= 24 ? (uint32_t)INT32_MAX : (128u << sh[j]) - 1u) : 0u;
             }
         }
         rc = upload(m, par, &D.par);

@@ -62,10 +62,10 @@ __device__ __forceinline__ v16i bias_tile(const uint32_t *blk, int j, int g) {
     return t;
 }
 
-// Requant parameters (M0, shift and pre-shift clamp bound; the bias is
-// already in the accumulators) of packed group g of n-tile j (lane half g2).
+// Requant parameters (M0 and shift; the bias is already in the accumulators)
+// of packed group g of n-tile j (lane half g2).
 struct RqPar {
-    v4i mm, hi;
+    v4i mm;
     uint32_t sh;
 };
 
@@ -74,27 +74,22 @@ __device__ __forceinline__ RqPar rq_par(const uint32_t *blk, int j, int g, int g
     const int o = 8 * g + 4 * g2;
     RqPar p;
     p.mm = *(const v4i *)(pj + 32 + o);
-    p.hi = *(const v4i *)(pj + 72 + o);
     p.sh = pj[64 + (o >> 2)];
     return p;
 }
 
-// Features 8g + 4*g2 + e (e = 0..3) of accumulator tiles acc[i], I0 <= i <
-// I1 (bias included) -> packed int8 words pk[i][g].  The byte inserts run
-// byte by byte across the words, so that consecutive inserts write
-// different registers.
-template <bool RELU, int I0, int I1, int RT>
-__device__ __forceinline__ void rq_words(const v16i (&acc)[RT], int g, const RqPar &p, uint32_t (&pk)[RT][4]) {
-    int y[4][RT];
+// Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile (bias included)
+// -> packed int8.
+template <bool RELU>
+__device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar &p) {
+    constexpr int lo = RELU ? 0 : -128;
+    uint32_t packed = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = I0; i < I1; ++i) y[e][i] = rq_clamp<RELU>(acc[i][4 * g + e], p.mm[e], p.hi[e]);
-    static_for<4>([&](auto ec) __attribute__((always_inline)) {
-        constexpr int e = decltype(ec)::value;
-#pragma unroll
-        for (int i = I0; i < I1; ++i) rq_insert<e>(pk[i][g], p.sh, y[e][i]);
-    });
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t q = requant_u8_fast(acc[4 * g + e], 0, p.mm[e], (p.sh >> (8 * e)) & 63u, lo);
+        packed |= q << (8 * e);
+    }
+    return packed;
 }
 
 __device__ __forceinline__ v4i wload_s(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
@@ -247,12 +242,14 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
             constexpr int j = v / 4, gg = v % 4;
             const RqPar cur = pp;
             if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
-            rq_words<true, 0, RT>(accB[j], gg, cur, pk[j]);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
         } else if constexpr (!LASTL && v >= 16) {
             constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
             const RqPar cur = pp;
             if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
-            rq_words<true, h * RH, (h ? RT : RH)>(accA[j], gg, cur, pk[j]);
+#pragma unroll
+            for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
         }
         // pass 1's bias tiles, one step before its first MFMAs
         if constexpr (!LASTL && v == KTH - 1) {
@@ -267,7 +264,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
             for (int i = 0; i < RT; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[set][slot][j], b[kt & 1][i],
                                                                   kt == 0 ? bias[j] : acc[j][i], 0, 0, 0);
-        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 3 + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
+        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 2 + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (v == 7) {
             // layer l-1 pass 1 -> region B; this layer's pass-1 and the next

@@ -149,10 +149,10 @@ def test_step_encoder_and_decoder_match_reference(int_models, name):
 
 
 def test_step_api_many_streams(int_models, oracle_mod):
-    """More rows and streams than one pass of the launch's workgroups covers
-    (2048 x 32 rows per pass of the persistent row loop): 150,001 CDF rows
-    against the oracle, and 70,001 streams x 3 encode / decode steps whose
-    decoder returns every coded symbol, with a few streams inactive."""
+    """Large batches, as the coder benchmark runs them: 150,001 CDF rows
+    (9,376 workgroups of 16 rows, the last one partial) against the oracle,
+    and 70,001 streams x 3 encode / decode steps whose decoder returns every
+    coded symbol, with every 1000th stream active for one step only."""
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder, int8_logits_to_cdf
     lut_np = int_models["lossless"].exp_lut
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -297,10 +297,10 @@ def test_plain_core_matches_oracle(oracle_mod, monkeypatch, which):
 
 @pytest.mark.parametrize("core", ["pipelined", "plain"])
 def test_fast_requant_clamp_bounds_match_oracle(oracle_mod, monkeypatch, core):
-    """Fast-path layers (every shift >= 32) whose per-channel shifts span
-    32..63: shift - 32 >= 24 (the pre-shift clamp bound held at INT32_MAX),
-    shifts that saturate most values at 127 and, on the output layer, at
-    -128, and shifts that leave 0 / -1."""
+    """Fast-path layers (every shift >= 32, mulhi(acc, m0) >> (shift - 32))
+    whose per-channel shifts span 32..63: shifts that saturate most values at
+    127 and, on the output layer, at -128, shifts that leave 0 / -1, and the
+    largest shifts (shift - 32 up to 31)."""
     from sigcomp_amd.model_io import make_layer, random_int_model
     from sigcomp_amd.quant_mlp_export import HipModel
     import dataclasses
