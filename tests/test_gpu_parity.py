@@ -332,11 +332,15 @@ def test_pipelined_core_selected_for_bundled_models(codecs):
     assert codecs["lossless"].hip.pipelined and codecs["lossy"].hip.pipelined
 
 
+@pytest.mark.parametrize("pair", ["auto", "0"])
 @pytest.mark.parametrize("units,extra", [(2, 7), (3, 0), (4, 31), (5, 1), (6, 500)])
-def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, units, extra):
+def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, monkeypatch, units, extra, pair):
     """Chunk counts that fill `units` full waves of 32-chunk row tiles per CU
     (split by the launch planner into 64/96/128-chunk workgroup launches)
-    plus a partial leftover launch; short random chunk lengths."""
+    plus leftover chunks, paired with the last launch's rows (auto) or in a
+    launch of their own (SC_HIP_DEC_PAIR=0); short random chunk lengths."""
+    if pair == "0":
+        monkeypatch.setenv("SC_HIP_DEC_PAIR", "0")
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
     n = units * 32 * n_cu + extra
     rng = np.random.default_rng(units * 1000 + extra)
