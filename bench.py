@@ -166,7 +166,7 @@ def bench_codec(args):
                      "traffic": pmc_traffic(args.config, "k_decompress"),
                      "traffic_source": f"profiles/traffic_{args.config}.txt (rocprofv3 PMC, bytes per launch)",
                      "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch",
-                     **ceiling_fields(achieved)},
+                     **ceiling_fields(achieved), **pmc_mfma(args.config, "k_decompress")},
     }
     return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
 
@@ -218,6 +218,27 @@ def pmc_traffic(config, kernel):
         if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == kernel:
             return int(f[2])
     return None
+
+
+def pmc_mfma(config, kernel):
+    """Counter-measured MFMA utilisation of `kernel` on this workload from the
+    committed rocprofv3 PMC summary (profiles/mfma_util.txt: fraction of
+    SIMD cycles the matrix cores are busy, and the clock), or {}."""
+    path = REPO / "profiles" / "mfma_util.txt"
+    if not path.exists():
+        return {}
+    out = {}
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if len(f) == 4 and f[1] == kernel and f[2] == config:
+            if f[0] == "mfma_busy":
+                out["mfma_busy_counters"] = float(f[3])
+            elif f[0] == "mfma_clock_ghz":
+                out["mfma_clock_ghz_counters"] = float(f[3])
+    if out:
+        out["mfma_counters_source"] = ("profiles/mfma_util.txt (rocprofv3 PMC SQ_VALU_MFMA_BUSY_CYCLES / "
+                                       "GRBM_GUI_ACTIVE, SQ_INSTS_VALU_MFMA_MOPS_I8)")
+    return out
 
 
 def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
@@ -322,7 +343,7 @@ def bench_mlp(args):
             "roofline": {"kernel": "k_mlp_context<cdf>", "bound": "mfma", "achieved": round(achieved, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                         **ceiling_fields(achieved)}}
+                         **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")}}
 
 
 def bench_ceiling(args):
