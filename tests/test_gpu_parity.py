@@ -357,6 +357,43 @@ def test_decompress_launch_plans(codecs, oracle_mod, oracle_models, monkeypatch,
     assert [words[woff[i]:woff[i] + wcnt[i]].tobytes() for i in sample] == ref
 
 
+def test_decompress_greedy_plan_uses_160_chunk_workgroups(codecs, capfd, monkeypatch):
+    """SC_HIP_DEC_PLAN=greedy with 6 units takes one launch of 160-chunk
+    workgroups (the plain core's rt = 5 kernel) and one of 32, then the
+    leftover chunks; every chunk round-trips."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    n = 6 * 32 * n_cu + 77
+    rng = np.random.default_rng(66)
+    lengths = rng.integers(1, 70, n).astype(np.int32)
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    monkeypatch.setenv("SC_HIP_DEC_PLAN", "greedy")
+    monkeypatch.setenv("SC_HIP_DEC_LOG", "1")
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "plan [5,1]" in log, log
+    assert np.array_equal(back, tokens)
+
+
+def test_decompress_one_million_chunks(codecs, capfd, monkeypatch):
+    """1,000,003 chunks of 1..6 tokens: a plan of many full-wave launches,
+    the decode state buffer grown to a million rows, and the length
+    statistics over all of them."""
+    rng = np.random.default_rng(7)
+    n = 1_000_003
+    lengths = rng.integers(1, 7, n).astype(np.int32)
+    tokens = rng.integers(0, 60, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossy"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    monkeypatch.setenv("SC_HIP_DEC_LOG", "1")
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    assert "chunks 1000003" in capfd.readouterr().err
+    assert np.array_equal(back, tokens)
+
+
 def _decode_direct(codec, words, woff, wcnt, lengths):
     """sc_decompress_chunks on the chunks in the order given (the C ABI does
     not sort) -> (tokens of all chunks in chunk order, per-chunk status).
