@@ -157,12 +157,14 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
                    int64_t *symbols_out, void *stream);
 
 /* Bytes of device workspace sc_compress_chunks needs for n_tokens tokens in
- * n_chunks chunks (a tile table, 4 bytes per chunk, and 8 bytes per token). */
+ * n_chunks chunks (a tile table, 4 bytes per chunk, tile descriptors, 16
+ * bytes per 128 tokens and per chunk, and 8 bytes per token). */
 int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks);
 
 /* Compress n_chunks independent token chunks (teacher-forced MLP over every
  * step fused with the logits -> frequency step, then the range encoder and
- * seal).  Chunk c: lengths[c] tokens (uint8) at tokens + tok_off[c]; its u32
+ * seal).  Chunk c: lengths[c] tokens (uint8) at tokens + tok_off[c]; chunks
+ * are disjoint and lie inside the n_tokens-byte token array; its u32
  * words go to words + word_off[c] (capacity word_cap[c] >= lengths[c] + 2 is
  * always sufficient); word_cnt[c] and status[c] are written.  All arrays
  * device.  Replaces QuantMLPCompression.compress_chunks /

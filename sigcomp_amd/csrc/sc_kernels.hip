@@ -67,18 +67,28 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     load_lut_lds(M.lut, s_lut);
     mlp_tile_init<PIPE>(M, s_par, wave, lane);
     const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
+    // A tile's 128 x 64 context tokens: 32 per thread, all loads issued
+    // before the first is used (a load / wait / store loop costs one memory
+    // round trip per token).  Element j * THREADS + thread is row 4j + wave,
+    // position lane: each load instruction reads 2 KB.  Addresses and row
+    // limits are formed from per-tile values, so that none is hoisted out of
+    // the tile loop (32 such registers held across the MLP make it spill).
+    constexpr int CTX_PER = R_TILE * WIN / THREADS;
+    static_assert(THREADS == 4 * WIN, "four context rows per load instruction");
     for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         const int64_t row0 = tile * R_TILE;
+        const int64_t *src = ctx + row0 * WIN + threadIdx.x;
+        const int64_t lim = rows - row0 - wave;   // element j is in range iff 4j < lim
+        int64_t v[CTX_PER];
+#pragma unroll
+        for (int j = 0; j < CTX_PER; ++j) v[j] = 4 * j < lim ? src[j * THREADS] : 0;
         __syncthreads();
         int bad = 0;
-        for (int i = threadIdx.x; i < R_TILE * WIN; i += THREADS) {
-            const int64_t row = row0 + i / WIN;
-            int64_t v = 0;
-            if (row < rows) {
-                v = ctx[row * WIN + (i % WIN)];
-                if (v < 0 || v > SOS) { bad = 1; v = 0; }
-            }
-            s_ctx[i] = (uint16_t)emb_off((int)v, 0);   // the MLP takes table addresses
+#pragma unroll
+        for (int j = 0; j < CTX_PER; ++j) {
+            const bool ok = (uint64_t)v[j] <= (uint64_t)SOS;
+            bad |= !ok;
+            s_ctx[j * THREADS + threadIdx.x] = (uint16_t)emb_off(ok ? (int)v[j] : 0, 0);   // table addresses
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
@@ -148,18 +158,40 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_tile_scan(const int32_t *__res
     if (threadIdx.x == SCAN_THREADS - 1) tile_start[n_chunks] = s_sum[SCAN_THREADS - 1];
 }
 
+// Tile descriptors, one thread per chunk: tile k of chunk c (global index
+// tile_start[c] + k) covers steps t0 = 128k .. t0 + 127 and is described by
+// {first token's index in the token array (low, high word), L - t0, t0}, so
+// that a compress workgroup finds its tile's tokens with one load instead of
+// a search over tile_start.
+__global__ __launch_bounds__(256) void k_tile_table(const int64_t *__restrict__ tok_off,
+                                                    const int32_t *__restrict__ lengths, int64_t n_chunks,
+                                                    const int32_t *__restrict__ tile_start, int4 *__restrict__ desc,
+                                                    int64_t max_desc) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n_chunks) return;
+    const int32_t L = lengths[c];
+    const int64_t base = tok_off[c];
+    int32_t k = tile_start[c];
+    // max_desc bounds the table for disjoint chunks inside the token array
+    for (int32_t t0 = 0; t0 < L && k < max_desc; t0 += R_TILE, ++k) {
+        const int64_t b = base + t0;
+        desc[k] = make_int4((int)(uint32_t)b, (int)(b >> 32), L - t0, t0);
+    }
+}
+
 // Workgroup b runs tiles b, b + G, b + 2G, ... (G = grid size) of the global
 // tile order.  Every tile costs the same, so the workgroups stay in step and
 // stream the same layer's weights at the same time: each XCD's L2 then
 // serves one weight fragment to all of its CUs (a work counter lets
 // workgroups drift apart, and the L2 cycles through the whole model).  A
-// tile's 128 + 64 tokens (64 of left context) are staged in LDS.  Output per
+// tile's 128 + 64 tokens (64 of left context) are staged in LDS from its
+// descriptor (k_tile_table), which is loaded while the previous tile's
+// frequency step runs, so a tile waits for one memory round trip.  Output per
 // token: (exclusive cumulative frequency, frequency) of the coded token.
 template <bool PIPE>
 __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
-                                                             const int64_t *__restrict__ tok_off,
-                                                             const int32_t *__restrict__ lengths,
                                                              int64_t n_chunks, const int32_t *__restrict__ tile_start,
+                                                             const int4 *__restrict__ desc, int64_t max_desc,
                                                              uint2 *__restrict__ pairs) {
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R_TILE / 4 is a multiple of EPI_N * WAVES
     static_assert((R_TILE / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must stay inside the tile");
@@ -170,42 +202,33 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ uint16_t s_apos[R_TILE + WIN];   // emb_off(s_tok[i], 0)
     __shared__ double s_lut[VOCAB];
-    __shared__ int64_t s_chunk;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
     mlp_tile_init<PIPE>(M, s_par, wave, lane);
-    const int32_t n_tiles = tile_start[n_chunks];
+    static_assert(R_TILE + WIN <= THREADS, "one staged token per thread");
+    const int32_t n_tiles = (int32_t)min<int64_t>(tile_start[n_chunks], max_desc);
+    // The next tile's descriptor is loaded during this tile's epilogue.
+    int4 d = (int32_t)blockIdx.x < n_tiles ? desc[blockIdx.x] : make_int4(0, 0, 0, 0);
     for (int32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            // last chunk c with tile_start[c] <= tile (chunks without tiles are skipped)
-            int64_t lo = 0, hi = n_chunks - 1;
-            while (lo < hi) {
-                const int64_t mid = (lo + hi + 1) >> 1;
-                if (tile_start[mid] <= tile) lo = mid;
-                else hi = mid - 1;
-            }
-            s_chunk = lo;
-        }
-        __syncthreads();
-        const int64_t c = s_chunk;
-        const int32_t L = lengths[c];
-        const int32_t t0 = (tile - tile_start[c]) * R_TILE;
-        const uint8_t *tk = tokens + tok_off[c];
-        uint2 *out = pairs + tok_off[c];
+        const int64_t base = (int64_t)(uint32_t)d.x | ((int64_t)d.y << 32);   // token t0 of the chunk
+        const int32_t rem = d.z, t0 = d.w;                                     // L - t0, t0
         // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
-        for (int i = threadIdx.x; i < R_TILE + WIN; i += THREADS) {
-            const int32_t pos = t0 - WIN + i;
-            const int v = pos < 0 ? SOS : (pos < L ? (int)tk[pos] : 0);
-            s_tok[i] = (uint16_t)v;
-            s_apos[i] = (uint16_t)emb_off(v, 0);
+        const int32_t p = (int32_t)threadIdx.x - WIN;
+        int v = 0;
+        if (threadIdx.x < R_TILE + WIN) v = t0 + p < 0 ? SOS : (p < rem ? (int)tokens[base + p] : 0);
+        __syncthreads();
+        if (threadIdx.x < R_TILE + WIN) {
+            s_tok[threadIdx.x] = (uint16_t)v;
+            s_apos[threadIdx.x] = (uint16_t)emb_off(v, 0);
         }
         __syncthreads();
         mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
                                 wave, lane);
-        const int32_t valid = min(R_TILE, L - t0);
+        if (tile + (int32_t)gridDim.x < n_tiles) d = desc[tile + gridDim.x];
+        uint2 *out = pairs + base;
+        const int32_t valid = min(R_TILE, rem);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.  The
         // lane holding the row's token publishes its 16 symbols in the row's
         // slot; the lane whose index is the token's low 4 bits stores its
@@ -230,7 +253,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
             for (int n = 0; n < EPI_N; ++n) {
                 uint32_t cum, freq;
                 slot_get(slots + (n * 4 + q4) * SLOT_DWORDS, u, cum, freq);
-                if (rr[n] < valid && (sym[n] & 15) == u) out[t0 + rr[n]] = make_uint2(cum, freq);
+                if (rr[n] < valid && (sym[n] & 15) == u) out[rr[n]] = make_uint2(cum, freq);
             }
         }
     }
@@ -1099,13 +1122,17 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
     return check_launch("k_decode_step");
 }
 
-// Workspace: tile_start (int32 [n_chunks + 1]), then the (cum, freq) pairs
+// Workspace: tile_start (int32 [n_chunks + 1]), the tile descriptors (int4
+// [at most n_tokens / 128 + n_chunks tiles]), then the (cum, freq) pairs
 // (8 bytes per token), each part 256-byte aligned.
 static int64_t tile_start_bytes(int64_t n_chunks) { return ((n_chunks + 1) * 4 + 255) / 256 * 256; }
+static int64_t tile_desc_bytes(int64_t n_tokens, int64_t n_chunks) {
+    return ((n_tokens / R_TILE + n_chunks) * 16 + 255) / 256 * 256;
+}
 
 int64_t sc_compress_workspace_bytes(int64_t n_tokens, int64_t n_chunks) {
     if (n_tokens < 0 || n_chunks < 0) return -1;
-    return tile_start_bytes(n_chunks) + ((n_tokens * 8 + 255) / 256) * 256;
+    return tile_start_bytes(n_chunks) + tile_desc_bytes(n_tokens, n_chunks) + ((n_tokens * 8 + 255) / 256) * 256;
 }
 
 int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *tok_off, const int32_t *lengths,
@@ -1121,17 +1148,22 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
     DeviceGuard guard(m->device);
     if (n_tokens / R_TILE + n_chunks >= (int64_t(1) << 31))
         return fail(SC_ERR_UNSUPPORTED, "more than 2**31 tiles");
+    const int64_t max_tiles = n_tokens / R_TILE + n_chunks;   // tiles of disjoint chunks of n_tokens tokens
     int32_t *tile_start = (int32_t *)workspace;
-    uint2 *pairs = (uint2 *)((char *)workspace + tile_start_bytes(n_chunks));
+    int4 *desc = (int4 *)((char *)workspace + tile_start_bytes(n_chunks));
+    uint2 *pairs = (uint2 *)((char *)desc + tile_desc_bytes(n_tokens, n_chunks));
     hipStream_t s = as_stream(stream);
     hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(SCAN_THREADS), 0, s, lengths, n_chunks, tile_start);
     int rc = check_launch("k_tile_scan");
     if (rc) return rc;
+    hipLaunchKernelGGL(k_tile_table, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, tok_off, lengths,
+                       n_chunks, tile_start, desc, max_tiles);
+    rc = check_launch("k_tile_table");
+    if (rc) return rc;
     // one workgroup per CU (or per tile when there are fewer tiles)
-    const int64_t max_tiles = n_tokens / R_TILE + n_chunks;
     const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(max_tiles, m->n_cu));
     hipLaunchKernelGGL(m->dev.pipe ? k_compress_mlp<true> : k_compress_mlp<false>, dim3(grid), dim3(THREADS), 0, s,
-                       m->dev, tokens, tok_off, lengths, n_chunks, tile_start, pairs);
+                       m->dev, tokens, n_chunks, tile_start, desc, max_tiles, pairs);
     rc = check_launch("k_compress_mlp");
     if (rc) return rc;
     hipLaunchKernelGGL(k_encode_pairs, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, pairs, tok_off,
