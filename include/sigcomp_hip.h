@@ -83,12 +83,15 @@ int sc_model_destroy(sc_model *model);
 /* Device copy of the model's exp LUT (uint64 [256]); owned by the model. */
 const uint64_t *sc_model_lut(const sc_model *model);
 
-/* MLP core the model runs on: 1 = pipelined core (every layer's requant
- * constants satisfy m0 < 2**31 and shift >= 32 after the m0 = 2**31
- * rewrite, ReLU on every layer but the last; tiles of up to 128 rows), 0 =
- * plain core (any valid model; also selected by SC_HIP_PLAIN_CORE=1 in the
- * environment at sc_model_create).  Both give identical results.  No
- * reference counterpart (diagnostic). */
+/* MLP core the model runs on: 2 = pipelined core with per-tensor requant
+ * (every layer's constants satisfy m0 < 2**31 and shift >= 32 after the
+ * m0 = 2**31 rewrite, ReLU on every layer but the last, and one m0 and
+ * shift per layer on all but the last, as in both bundled checkpoints;
+ * tiles of up to 128 rows; every kernel), 1 = pipelined core with
+ * per-channel constants (the explicit-context kernels; compress and
+ * decompress run the plain core), 0 = plain core (any valid model; also
+ * selected by SC_HIP_PLAIN_CORE=1 in the environment at sc_model_create).
+ * All give identical results.  No reference counterpart (diagnostic). */
 int sc_model_core(const sc_model *model);
 
 /* MLP forward on explicit context windows: ctx int64 [rows, 64] (device,

@@ -51,7 +51,9 @@ struct LayerDev {
     int32_t relu;
     int32_t bytes;           // size of the packed weight buffer
     int32_t fast;            // every m0 < 2**31 and shift >= 32; shift[] holds shift - 32
-    int32_t pad;
+    int32_t uni;             // fast, and one m0 and shift for every output (per-tensor constants):
+    int32_t um0, ush;        //   that m0 and shift - 32
+    int32_t uhi;             //   the pre-shift clamp bound min(128 * 2**ush - 1, 2**31 - 1)
 };
 
 struct ModelDev {
@@ -59,8 +61,14 @@ struct ModelDev {
     const int8_t *emb;       // [257][128] row-major
     const uint64_t *lut;     // [256]
     int32_t n_layers;
-    int32_t pipe;            // every layer fast, ReLU on all but the last: pipelined core usable
+    int32_t pipe;            // MLP core: CORE_PLAIN, CORE_PIPE or CORE_PIPE_UNI (sc_model_create)
 };
+
+// MLP cores.  CORE_PIPE (sc_pipe.h) needs every layer fast with ReLU on all
+// but the last; CORE_PIPE_UNI additionally per-tensor constants on every
+// layer but the last (their requantisation then takes four VALU
+// instructions per value, rq_word_uni).  All three give identical results.
+constexpr int CORE_PLAIN = 0, CORE_PIPE = 1, CORE_PIPE_UNI = 2;
 
 // ---------------------------------------------------------------- LDS layouts
 

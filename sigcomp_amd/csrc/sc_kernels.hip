@@ -32,10 +32,10 @@ constexpr int DEC_RT_MAX = 5;       // decode: up to 160 chunks per workgroup (L
 enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
 
 // MLP core of one tile: the pipelined core when the model allows it.
-template <bool PIPE, int RT, class AposFn>
+template <int CORE, int RT, class AposFn>
 __device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act, uint32_t *s_par,
                                          AposFn apos, int wave, int lane) {
-    if constexpr (PIPE) mlp_rows_pipe<RT>(M, s_emb, s_act, s_par, apos, wave, lane);
+    if constexpr (CORE != CORE_PLAIN) mlp_rows_pipe<RT, CORE == CORE_PIPE_UNI>(M, s_emb, s_act, s_par, apos, wave, lane);
     else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, apos, wave, lane);
 }
 // once per kernel, before the first mlp_tile (and a barrier)
@@ -51,11 +51,12 @@ constexpr int act_row_bytes() { return PIPE ? PACT_ROW : ACT_ROW; }
 template <bool PIPE>
 __device__ __forceinline__ int act_at(int r, int chunk) { return PIPE ? pact_off(r, chunk) : act_off(r, chunk); }
 
-template <int MODE, bool PIPE>
+template <int MODE, int CORE>
 __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const int64_t *__restrict__ ctx,
                                                             int64_t rows, int8_t *__restrict__ logits,
                                                             int32_t *__restrict__ cdf,
                                                             int32_t *__restrict__ status) {
+    constexpr bool PIPE = CORE != CORE_PLAIN;
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
-        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
                                 wave, lane);
         if (MODE == OUT_LOGITS) {
             // 128 rows x 256 bytes, 16-byte chunks, coalesced
@@ -188,11 +189,12 @@ __global__ __launch_bounds__(256) void k_tile_table(const int64_t *__restrict__ 
 // descriptor (k_tile_table), which is loaded while the previous tile's
 // frequency step runs, so a tile waits for one memory round trip.  Output per
 // token: (exclusive cumulative frequency, frequency) of the coded token.
-template <bool PIPE>
+template <int CORE>
 __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
                                                              int64_t n_chunks, const int32_t *__restrict__ tile_start,
                                                              const int4 *__restrict__ desc, int64_t max_desc,
                                                              uint2 *__restrict__ pairs) {
+    constexpr bool PIPE = CORE != CORE_PLAIN;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R_TILE / 4 is a multiple of EPI_N * WAVES
     static_assert((R_TILE / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must stay inside the tile");
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
             s_apos[threadIdx.x] = (uint16_t)emb_off(v, 0);
         }
         __syncthreads();
-        mlp_tile<PIPE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
+        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
                                 wave, lane);
         if (tile + (int32_t)gridDim.x < n_tiles) d = desc[tile + gridDim.x];
         uint2 *out = pairs + base;
@@ -311,7 +313,7 @@ __device__ __forceinline__ uint64_t dec_init_point(const uint32_t *w, int cnt, i
     return point;
 }
 
-template <int RT, bool PIPE>
+template <int RT, int CORE>
 __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
                                                            const int64_t *__restrict__ word_off,
                                                            const int32_t *__restrict__ word_cnt,
@@ -326,6 +328,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     // 2 * n_chunks - 1 - c (the n_second chunks after the launch's own, in
     // reverse order, so that with chunks sorted longest first the longest
     // second chunk follows the shortest first chunk).
+    constexpr bool PIPE = CORE != CORE_PLAIN;
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
     static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
@@ -425,7 +428,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         __syncthreads();
     }
     for (int32_t t = t_begin; t < t_stop; ++t) {
-        mlp_tile<PIPE, RT>(M, s_emb, s_act, s_par,
+        mlp_tile<CORE, RT>(M, s_emb, s_act, s_par,
                            [&](int r, int p) {
                                const int q = r * WIN + ((t + p) & (WIN - 1));
                                if (t + p < WIN) return emb_off(SOS, 0);
@@ -904,7 +907,8 @@ template <int RT>
 void dec_launch(const sc_model *m, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                 const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
                 int32_t *st, DecState *state, int32_t t_begin, int32_t t_end, int64_t n_second) {
-    auto *kern = m->dev.pipe && RT <= 4 ? k_decompress<RT, (RT <= 4)> : k_decompress<RT, false>;
+    auto *kern = m->dev.pipe == CORE_PIPE_UNI && RT <= 4 ? k_decompress<RT, (RT <= 4 ? CORE_PIPE_UNI : CORE_PLAIN)>
+                                                         : k_decompress<RT, CORE_PLAIN>;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, s, m->dev, words, woff, wcnt, len, count, tokens, toff,
                        st, state, t_begin, t_end, n_second);
 }
@@ -1001,6 +1005,13 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         if (fast)
             for (int j = 0; j < L.n; ++j) sh[j] = (uint8_t)(sh[j] - 32);
         D.fast = fast ? 1 : 0;
+        // per-tensor constants: one m0 and shift for the whole layer
+        bool uni = fast;
+        for (int j = 1; j < L.n && uni; ++j) uni = m0[j] == m0[0] && sh[j] == sh[0];
+        D.uni = uni ? 1 : 0;
+        D.um0 = uni ? (int32_t)m0[0] : 0;
+        D.ush = uni ? sh[0] : 0;
+        D.uhi = uni ? (int32_t)std::min<int64_t>((int64_t(128) << sh[0]) - 1, INT32_MAX) : 0;
         std::vector<uint32_t> par((size_t)(L.n / 32) * PAR_DWORDS, 0u);
         for (int nt = 0; nt < L.n / 32; ++nt) {
             uint32_t *blk = par.data() + (size_t)nt * PAR_DWORDS;
@@ -1021,9 +1032,12 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     m->dev.n_layers = n_layers;
     // SC_HIP_PLAIN_CORE=1 at model creation selects the plain core (testing)
     const char *plain = getenv("SC_HIP_PLAIN_CORE");
-    m->dev.pipe = plain && plain[0] == '1' ? 0 : 1;
-    for (int i = 0; i < n_layers; ++i)
-        if (!m->dev.layer[i].fast || m->dev.layer[i].relu != (i < n_layers - 1 ? 1 : 0)) m->dev.pipe = 0;
+    bool pipe = !(plain && plain[0] == '1'), uni = true;
+    for (int i = 0; i < n_layers; ++i) {
+        if (!m->dev.layer[i].fast || m->dev.layer[i].relu != (i < n_layers - 1 ? 1 : 0)) pipe = false;
+        if (i < n_layers - 1 && !m->dev.layer[i].uni) uni = false;
+    }
+    m->dev.pipe = !pipe ? CORE_PLAIN : uni ? CORE_PIPE_UNI : CORE_PIPE;
     if (rc != SC_OK) {
         sc_model_destroy(m);
         return rc;
@@ -1045,7 +1059,7 @@ int sc_model_destroy(sc_model *m) {
 
 const uint64_t *sc_model_lut(const sc_model *m) { return m ? m->dev.lut : nullptr; }
 
-int sc_model_core(const sc_model *m) { return m && m->dev.pipe ? 1 : 0; }
+int sc_model_core(const sc_model *m) { return m ? m->dev.pipe : 0; }
 
 static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t rows, int8_t *logits,
                               int32_t *cdf, int32_t *status, void *stream, int mode) {
@@ -1056,8 +1070,13 @@ static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t row
     DeviceGuard guard(m->device);
     const int64_t tiles = (rows + R_TILE - 1) / R_TILE;
     const int grid = (int)std::min<int64_t>(tiles, m->n_cu);
-    auto *kern = mode == OUT_LOGITS ? (m->dev.pipe ? k_mlp_context<OUT_LOGITS, true> : k_mlp_context<OUT_LOGITS, false>)
-                                    : (m->dev.pipe ? k_mlp_context<OUT_CDF32, true> : k_mlp_context<OUT_CDF32, false>);
+    auto *kern = mode == OUT_LOGITS
+                     ? (m->dev.pipe == CORE_PIPE_UNI ? k_mlp_context<OUT_LOGITS, CORE_PIPE_UNI>
+                        : m->dev.pipe == CORE_PIPE   ? k_mlp_context<OUT_LOGITS, CORE_PIPE>
+                                                     : k_mlp_context<OUT_LOGITS, CORE_PLAIN>)
+                     : (m->dev.pipe == CORE_PIPE_UNI ? k_mlp_context<OUT_CDF32, CORE_PIPE_UNI>
+                        : m->dev.pipe == CORE_PIPE   ? k_mlp_context<OUT_CDF32, CORE_PIPE>
+                                                     : k_mlp_context<OUT_CDF32, CORE_PLAIN>);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, as_stream(stream), m->dev, ctx, rows, logits, cdf,
                        status);
     return check_launch("k_mlp_context");
@@ -1162,7 +1181,10 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
     if (rc) return rc;
     // one workgroup per CU (or per tile when there are fewer tiles)
     const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(max_tiles, m->n_cu));
-    hipLaunchKernelGGL(m->dev.pipe ? k_compress_mlp<true> : k_compress_mlp<false>, dim3(grid), dim3(THREADS), 0, s,
+    // compress and decompress run the pipelined core only with per-tensor
+    // constants (the bundled checkpoints); other models take the plain core
+    hipLaunchKernelGGL(m->dev.pipe == CORE_PIPE_UNI ? k_compress_mlp<CORE_PIPE_UNI> : k_compress_mlp<CORE_PLAIN>,
+                       dim3(grid), dim3(THREADS), 0, s,
                        m->dev, tokens, n_chunks, tile_start, desc, max_tiles, pairs);
     rc = check_launch("k_compress_mlp");
     if (rc) return rc;
@@ -1200,7 +1222,8 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     // Launch plan.  A workgroup owns 32*rt consecutive chunks for the whole
     // decode, one workgroup per CU, and every launch but the last is one
     // full wave of n_cu workgroups.  The chunks of the full waves make
-    // `units` row tiles per CU; with the pipelined core they are split into
+    // `units` row tiles per CU; with the pipelined core (per-tensor
+    // constants: every kernel runs it) they are split into
     // launches by dec_plan (measured step costs), otherwise taken greedily
     // at the largest rt.  The chunks left over (fewer than 32*n_cu) either
     // follow the last rows of the last full-wave launch in the same rows
@@ -1212,7 +1235,7 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     const int64_t units = n_chunks / (32 * cu);
     std::vector<int> plan;
     const char *plan_env = getenv("SC_HIP_DEC_PLAN");   // "greedy": largest rt first (comparisons)
-    if (m->dev.pipe && !(plan_env && std::strcmp(plan_env, "greedy") == 0)) {
+    if (m->dev.pipe == CORE_PIPE_UNI && !(plan_env && std::strcmp(plan_env, "greedy") == 0)) {
         plan = dec_plan(units);
     } else {
         for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, DEC_RT_MAX))
@@ -1222,7 +1245,7 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     const int rt_last = plan.empty() ? 0 : plan.back();
     const int64_t g_count = (int64_t)rt_last * 32 * cu, g0 = units * 32 * cu - g_count;
     const char *pair_env = getenv("SC_HIP_DEC_PAIR");   // "0": never pair (comparisons)
-    const bool can_pair = m->dev.pipe && rt_last >= 1 && rt_last <= 4 && left > 0 && left <= g_count &&
+    const bool can_pair = m->dev.pipe == CORE_PIPE_UNI && rt_last >= 1 && rt_last <= 4 && left > 0 && left <= g_count &&
                           !(pair_env && std::strcmp(pair_env, "0") == 0);
     // step segments (SC_HIP_DEC_SEG overrides the length, 0 = one launch per
     // group): the longest row bounds the segments of every group

@@ -21,6 +21,8 @@
 //   boundaries.  Accumulators of the two passes take 2 x 2 x RT x 16 AGPRs
 //   (256 for RT = 4).
 //
+// With UNI (CORE_PIPE_UNI: per-tensor constants on every layer but the
+// last) the interleaved requantisation is rq_words_uni, else rq_word.
 // Requires every layer to take the 32-bit requant path (LayerDev::fast), ReLU
 // on all layers but the last, and 512-wide hidden layers (ModelDev::pipe).
 #pragma once
@@ -90,6 +92,53 @@ __device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar 
         packed |= q << (8 * e);
     }
     return packed;
+}
+
+// Per-tensor constants (LayerDev::uni): x = hi32(a * m0) is clamped to
+// [0, uhi] BEFORE the shift, uhi = 128 * 2**sh - 1 (or 2**31 - 1 when that
+// overflows; then x >> sh < 128 anyway).  floor(x / 2**sh) is monotone in
+// x, so this equals min(max(x >> sh, 0), 127) of rq_word<true>; the shift
+// then writes each byte straight into the packed word (SDWA destination
+// select; byte 0 clears the others).  Four VALU instructions per value with
+// the accumulator read, and no per-channel operands.
+struct RqUni {
+    int m0, hi, sh;
+};
+__device__ __forceinline__ RqUni rq_uni(const LayerDev &L) {
+    return RqUni{__builtin_amdgcn_readfirstlane(L.um0), __builtin_amdgcn_readfirstlane(L.uhi),
+                 __builtin_amdgcn_readfirstlane(L.ush)};
+}
+template <int E>
+__device__ __forceinline__ void rq_insert_uni(uint32_t &packed, int sh, int y) {
+    if constexpr (E == 0)
+        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+            : "=v"(packed) : "v"(sh), "v"(y));
+    else if constexpr (E == 1)
+        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(packed) : "v"(sh), "v"(y));
+    else if constexpr (E == 2)
+        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(packed) : "v"(sh), "v"(y));
+    else
+        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+            : "+v"(packed) : "v"(sh), "v"(y));
+}
+// Features 8g + 4*g2 + e (e = 0..3) of accumulator tiles acc[i], I0 <= i <
+// I1 -> packed words pk[i][g].  The inserts run byte by byte across the
+// words, so that consecutive inserts write different registers.
+template <int I0, int I1, int RT>
+__device__ __forceinline__ void rq_words_uni(const v16i (&acc)[RT], int g, const RqUni &p, uint32_t (&pk)[RT][4]) {
+    int y[4][RT];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = I0; i < I1; ++i)
+            asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "s"(p.hi));
+    static_for<4>([&](auto ec) __attribute__((always_inline)) {
+        constexpr int e = decltype(ec)::value;
+#pragma unroll
+        for (int i = I0; i < I1; ++i) rq_insert_uni<e>(pk[i][g], p.sh, y[e][i]);
+    });
 }
 
 __device__ __forceinline__ v4i wload_s(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
@@ -190,8 +239,8 @@ __device__ __forceinline__ void pipe_schedule() {
 // slot_p1(l) = its parameters, slot_p0(l+1) = the next layer's pass-0
 // parameters, region A = this layer's pass 0 (visible), w[0][*] = the next
 // layer's first k-steps.  Both passes' GEMMs start from their bias tiles.
-template <int RT, bool LASTL>
-__device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
+template <int RT, bool LASTL, bool UNI>
+__device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
                                             uint32_t *s_parw, int l, v16i (&accA)[PNT][RT],
                                             v16i (&accB)[PNT][RT], v4i (&w)[2][PPD][PNT],
                                             uint32_t (&pk)[PNT][RT][4], int wave, int lane) {
@@ -214,7 +263,13 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
     }
     v4i b[2][RT];
     read_b<RT>(s_act, bbase, 0, b[0]);
-    RqPar pp = rq_par(prev1, 0, 0, g);
+    RqPar pp;
+    if constexpr (!UNI) pp = rq_par(prev1, 0, 0, g);
+    RqUni up{}, uc{};
+    if constexpr (UNI) {
+        up = rq_uni(Lp);
+        uc = rq_uni(L);
+    }
     v16i bias[PNT];
 #pragma unroll
     for (int j = 0; j < PNT; ++j) bias[j] = bias_tile(cur0, j, g);
@@ -240,16 +295,24 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
         constexpr int VA = v < 8 ? 12 : (!LASTL && v >= 16 ? 6 : 0);
         if constexpr (v < 8) {
             constexpr int j = v / 4, gg = v % 4;
-            const RqPar cur = pp;
-            if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
+            if constexpr (UNI) {
+                rq_words_uni<0, RT>(accB[j], gg, up, pk[j]);
+            } else {
+                const RqPar cur = pp;
+                if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
 #pragma unroll
-            for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
+                for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
+            }
         } else if constexpr (!LASTL && v >= 16) {
             constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
-            const RqPar cur = pp;
-            if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
+            if constexpr (UNI) {
+                rq_words_uni<h * RH, (h ? RT : RH)>(accA[j], gg, uc, pk[j]);
+            } else {
+                const RqPar cur = pp;
+                if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
 #pragma unroll
-            for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
+                for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
+            }
         }
         // pass 1's bias tiles, one step before its first MFMAs
         if constexpr (!LASTL && v == KTH - 1) {
@@ -264,7 +327,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
             for (int i = 0; i < RT; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[set][slot][j], b[kt & 1][i],
                                                                   kt == 0 ? bias[j] : acc[j][i], 0, 0, 0);
-        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + 2 + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
+        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + (UNI ? 0 : 2) + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (v == 7) {
             // layer l-1 pass 1 -> region B; this layer's pass-1 and the next
@@ -273,7 +336,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
             if constexpr (!LASTL) {
                 par_put(cur1, pr1, lane);
                 par_put(next0, prn, lane);
-                pp = rq_par(cur0, 0, 0, g);   // first parameters of the pass-0 requantisation
+                if constexpr (!UNI) pp = rq_par(cur0, 0, 0, g);   // first parameters of the pass-0 requantisation
             }
             __syncthreads();
             read_b<RT>(s_act, bbase, 8, b[0]);
@@ -295,7 +358,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &L, const LayerDev &L
 // of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of
 // each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS,
 // layer 0's slots filled by pipe_params_init.
-template <int RT, class AposFn>
+template <int RT, bool UNI, class AposFn>
 __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
                                               uint32_t *s_par, AposFn apos, int wave, int lane) {
     static_assert(RT >= 1 && RT <= 4, "two passes of accumulators must fit the AGPRs");
@@ -344,8 +407,10 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     const int last = M.n_layers - 1;
 #pragma unroll 1
     for (int l = 1; l < last; ++l)
-        pipe_hidden<RT, false>(M.layer[l], M.layer[l + 1], s_act, s_parw, l, accA, accB, w, pk, wave, lane);
-    pipe_hidden<RT, true>(M.layer[last], M.layer[last], s_act, s_parw, last, accA, accB, w, pk, wave, lane);
+        pipe_hidden<RT, false, UNI>(M.layer[l - 1], M.layer[l], M.layer[l + 1], s_act, s_parw, l, accA, accB, w, pk,
+                                    wave, lane);
+    pipe_hidden<RT, true, UNI>(M.layer[last - 1], M.layer[last], M.layer[last], s_act, s_parw, last, accA, accB, w,
+                               pk, wave, lane);
 }
 
 }  // namespace sc

@@ -69,8 +69,11 @@ class HipModel:
                                                   ctypes.byref(handle)))
         self.handle = handle
         self.exp_lut = torch.from_numpy(lut.copy()).to(self.device)
-        # True when the kernels run the pipelined MLP core (see sc_model_core)
-        self.pipelined = bool(_hip.lib().sc_model_core(handle))
+        # MLP core of the kernels (sc_model_core): 2 = pipelined with per-tensor
+        # requant constants (every kernel), 1 = pipelined for the explicit-context
+        # kernels only, 0 = plain
+        self.core = int(_hip.lib().sc_model_core(handle))
+        self.pipelined = self.core != 0
 
     def __del__(self):
         h = getattr(self, "handle", None)

@@ -328,8 +328,64 @@ def test_fast_requant_clamp_bounds_match_oracle(oracle_mod, monkeypatch, core):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("shift", [32, 33, 38, 56, 63])
+def test_per_tensor_requant_matches_oracle(oracle_mod, shift):
+    """Per-tensor constants (one m0 and shift per layer, as in the bundled
+    checkpoints) select core 2, whose hidden-layer requantisation clamps
+    before the shift against a per-layer bound and shifts into the packed
+    byte.  Layer 2's shift: 32 (most values saturate at 127), 33, 38, 56
+    (the bound 128 * 2**24 - 1 exceeds int32 and is capped) and 63; layer 0
+    (requantised by both paths: pass 0 per channel, pass 1 per tensor) keeps
+    its drawn constants.  Logits, CDFs, chunk bytes and the round trip are
+    compared with the oracle."""
+    import dataclasses
+    from sigcomp_amd.model_io import make_layer, random_int_model
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    m = random_int_model(seed=17, per_channel=False)
+    rng = np.random.default_rng(17)
+    layers = list(m.layers)
+    L = layers[2]
+    m0 = int(rng.integers(1 << 30, 1 << 31))
+    layers[2] = make_layer(L.weight, L.bias, np.full(L.n, m0), np.full(L.n, shift, np.int32), True)
+    model = dataclasses.replace(m, layers=layers)
+    codec = QuantMLPCompression(chunk_len=2048, gpu=0, model=model)
+    assert codec.hip.core == 2
+    om = oracle_mod.OracleModel(model)
+    ctx = rng.integers(0, 257, (300, 64))
+    ctx[:40, :25] = 256
+    exp = oracle_mod.mlp_forward(om, ctx)
+    got = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
+    assert np.array_equal(got, exp)
+    cdf = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "cdf").cpu().numpy()
+    assert np.array_equal(cdf.astype(np.int64), oracle_mod.logits_to_cdf(exp, model.exp_lut))
+    lengths = [1, 64, 129, 700]
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    gpu = codec.compress_chunks(chunks)
+    assert gpu == oracle_mod.compress_chunks(om, chunks)
+    back = codec.decompress_chunks(gpu, lengths)
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+
+
+def test_per_channel_model_runs_plain_core_in_codec(oracle_mod):
+    """A pipelined-capable model with per-channel constants runs core 1: the
+    pipelined core in the explicit-context kernels, the plain core in
+    compress / decompress; chunk bytes still equal the oracle's."""
+    from sigcomp_amd.model_io import random_int_model
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    model = random_int_model(seed=23, per_channel=True)
+    codec = QuantMLPCompression(chunk_len=2048, gpu=0, model=model)
+    assert codec.hip.core == 1
+    rng = np.random.default_rng(23)
+    lengths = [2, 65, 333]
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    gpu = codec.compress_chunks(chunks)
+    assert gpu == oracle_mod.compress_chunks(oracle_mod.OracleModel(model), chunks)
+    back = codec.decompress_chunks(gpu, lengths)
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+
+
 def test_pipelined_core_selected_for_bundled_models(codecs):
-    assert codecs["lossless"].hip.pipelined and codecs["lossy"].hip.pipelined
+    assert codecs["lossless"].hip.core == 2 and codecs["lossy"].hip.core == 2
 
 
 @pytest.mark.parametrize("pair", ["auto", "0"])

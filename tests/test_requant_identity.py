@@ -36,3 +36,17 @@ def test_m0_two_pow_31_rewrite():
             a = int(a)
             assert floor_shift(a, 2**31, s) == floor_shift(a, 2**30, s - 1)
 
+
+
+def test_clamp_before_shift_identity():
+    """Per-tensor path: x = mulhi(acc, m0) clamped to [0, hi] and then
+    shifted by sh = shift - 32 equals the clamp of x >> sh to [0, 127], with
+    hi = 128 * 2**sh - 1 capped at 2**31 - 1 (the int32 range of the
+    register; for sh >= 24 every int32 x has x >> sh < 128)."""
+    rng = np.random.default_rng(2)
+    xs = [-(2**31), -(2**31) + 1, -1, 0, 1, 2**31 - 1] + [int(v) for v in rng.integers(-2**31, 2**31, 4000)]
+    for sh in range(32):
+        hi = min(128 * 2**sh - 1, 2**31 - 1)
+        edges = [hi - 1, hi, hi + 1, 127 * 2**sh - 1, 127 * 2**sh, 128 * 2**sh]
+        for x in xs + [e for e in edges if -(2**31) <= e < 2**31]:
+            assert min(max(x >> sh, 0), 127) == (min(max(x, 0), hi) >> sh)
