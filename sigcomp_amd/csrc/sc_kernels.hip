@@ -881,9 +881,10 @@ hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
 // Per-step cost of a full-wave decode launch at rt = 1 .. DEC_RT_MAX row
 // tiles per workgroup (MI355X, 512-token chunks, lossless model; us x 10 per
-// step; rt <= 4 runs the pipelined core).  Per row tile rt = 3 and 4 are
-// cheapest (40.3 us), rt = 1 the dearest (67.9 us).
-constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 679, 881, 1210, 1614, 2221};
+// step; rt <= 4 runs the pipelined core with per-tensor requantisation).
+// Per row tile rt = 3 and 4 are cheapest (38.5 and 39.0 us), rt = 1 the
+// dearest (66.6 us).
+constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 666, 824, 1156, 1561, 2154};
 
 // Split `units` row tiles per CU into launch sizes of least summed step cost
 // (largest first, so that they take the longest chunks).
