@@ -1,6 +1,6 @@
 """SigComp codec benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c2|ceiling|coder]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c1|c2|ceiling|coder]
 
 Default workload (config c3+c4): 4,000 seeded synthetic R10.4.1-like reads
 (~80 M int16 samples), bundled lossless model, chunk_len 2048.  One step =
@@ -14,7 +14,9 @@ Prints one JSON line: value = round-trip Msamples/s (samples / (compress +
 decompress time)); compress and decompress rates, bits/sample, the
 roofline of the dominant kernel (k_decompress, int8 MFMA bound) measured
 with HIP events on its own stream, and the CPU oracle baseline on a bounded
-sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c2 = MLP
+sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c1 = the
+reference's CPU-runnable case (64 reads, lossless), with the CPU oracle run
+over the whole workload and every chunk's bytes compared; c2 = MLP
 microbenchmark (1,048,576 context rows -> int32 CDF tables); ceiling = the
 int8 MFMA rate the GPU sustains at its power limit (register-operand MFMA
 chains on every CU, random and zero operands), recorded in
@@ -301,6 +303,39 @@ def cpu_baseline(model, chunks, gpu_words, word_off, word_cnt, samples_per_token
                       f"together ({dtoks} tokens, {td:.1f} s); C oracle on {threads} threads"}
 
 
+def cpu_full(model, chunks, gpu_words, word_off, word_cnt, samples):
+    """Config c1 (the reference's CPU-runnable case): the CPU oracle over the
+    whole workload, all host threads, and every chunk checked.  Compress:
+    every chunk, bytes compared with the GPU's; decompress: every GPU stream
+    decoded autoregressively, batched across chunks, tokens compared with
+    the originals.  About a minute on 16 host threads."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    threads = oracle.cpu_count()
+    oracle.set_num_threads(threads)
+    om = oracle.OracleModel(model)
+    t0 = time.perf_counter()
+    ref = oracle.compress_chunks(om, chunks)
+    tc = time.perf_counter() - t0
+    streams = [gpu_words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in range(len(chunks))]
+    bad = [i for i in range(len(chunks)) if streams[i] != ref[i]]
+    if bad:
+        raise RuntimeError(f"{len(bad)} chunks differ from the CPU oracle (first {bad[0]})")
+    t0 = time.perf_counter()
+    dec = oracle.decompress_chunks(om, streams, [len(c) for c in chunks])
+    td = time.perf_counter() - t0
+    if not all(np.array_equal(d, c) for d, c in zip(dec, chunks)):
+        raise RuntimeError("CPU oracle decode disagrees with the GPU streams")
+    c_rate, d_rate = samples / tc, samples / td
+    return {"value": round(samples / (tc + td) / 1e6, 5),
+            "unit": "Msamples/s (round trip)", "cores": threads, "kind": "port",
+            "compress_msamples_s": round(c_rate / 1e6, 5),
+            "decompress_msamples_s": round(d_rate / 1e6, 5),
+            "sample": f"the whole workload: {len(chunks)} chunks compressed ({tc:.1f} s) and decoded "
+                      f"({td:.1f} s) by the C oracle on {threads} threads; all {len(chunks)} chunk byte "
+                      f"strings equal the GPU's"}
+
+
 def bench_mlp(args):
     """Config c2: 1,048,576 context rows -> int32 CDF tables, seeded random
     per-channel model with the bundled checkpoints' layer dims."""
@@ -516,7 +551,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c2", "ceiling", "coder"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c1", "c2", "ceiling", "coder"])
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -542,7 +577,11 @@ def main():
         model = load_int_model(DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy"
                                else DEFAULT_QUANT_LOSSLESS_MODEL_PATH)
         log("[bench] cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(model, chunks, *gpu_out, samples / res["config"]["tokens"])
+        if args.config == "c1":
+            res["cpu_baseline"] = cpu_full(model, chunks, *gpu_out, samples)
+            res["parity"]["oracle_all_chunks"] = len(chunks)
+        else:
+            res["cpu_baseline"] = cpu_baseline(model, chunks, *gpu_out, samples / res["config"]["tokens"])
     print(json.dumps(res), flush=True)
 
 
