@@ -59,7 +59,11 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     constexpr bool PIPE = CORE != CORE_PLAIN;
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
-    __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * WIN];
+    // rows padded to CTX_STRIDE halfwords: layer 0 reads one position of 32
+    // consecutive rows at a time, which a 128-byte row stride would put in
+    // one LDS bank
+    constexpr int CTX_STRIDE = WIN + 2;
+    __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * CTX_STRIDE];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -89,11 +93,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
         for (int j = 0; j < CTX_PER; ++j) {
             const bool ok = (uint64_t)v[j] <= (uint64_t)SOS;
             bad |= !ok;
-            s_ctx[j * THREADS + threadIdx.x] = (uint16_t)emb_off(ok ? (int)v[j] : 0, 0);   // table addresses
+            // element j * THREADS + thread: row 4j + wave, position lane
+            s_ctx[(4 * j + wave) * CTX_STRIDE + lane] = (uint16_t)emb_off(ok ? (int)v[j] : 0, 0);   // table addresses
         }
         if (bad) status[0] = SC_STATUS_BAD_TOKEN;
         __syncthreads();
-        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * WIN + p]; },
+        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * CTX_STRIDE + p]; },
                                 wave, lane);
         if (MODE == OUT_LOGITS) {
             // 128 rows x 256 bytes, 16-byte chunks, coalesced
@@ -336,8 +341,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R * act_row_bytes<PIPE>()];
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
     // the pipelined core also keeps the ring as embedding-table addresses
-    // (emb_off(token, 0)), written with the token; the plain core converts
+    // (emb_off(token, 0)), written with the token; the plain core converts.
+    // Position-major (apos_at): layer 0 reads one position of 32 consecutive
+    // rows at a time, 32 consecutive halfwords instead of 32 reads 128 bytes
+    // apart in one LDS bank.
     __shared__ __attribute__((aligned(16))) uint16_t s_apos[PIPE ? R * WIN : 1];
+    auto apos_at = [](int r, int32_t pos) { return (pos & (WIN - 1)) * R + r; };
     __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
     __shared__ double s_lut[VOCAB];
@@ -422,7 +431,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                 // steps before the current chunk started are its start-of-sequence context
                 const int v = rs >= 0 ? (int)tokens[s_toff[r] + rs] : SOS;
                 s_ring[r * WIN + (tp & (WIN - 1))] = (uint8_t)v;
-                if constexpr (PIPE) s_apos[r * WIN + (tp & (WIN - 1))] = (uint16_t)emb_off(v, 0);
+                if constexpr (PIPE) s_apos[apos_at(r, tp)] = (uint16_t)emb_off(v, 0);
             }
         }
         __syncthreads();
@@ -430,10 +439,9 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     for (int32_t t = t_begin; t < t_stop; ++t) {
         mlp_tile<CORE, RT>(M, s_emb, s_act, s_par,
                            [&](int r, int p) {
-                               const int q = r * WIN + ((t + p) & (WIN - 1));
                                if (t + p < WIN) return emb_off(SOS, 0);
-                               if constexpr (PIPE) return (int)s_apos[q];
-                               else return emb_off(s_ring[q], 0);
+                               if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
+                               else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
                            },
                            wave, lane);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
@@ -498,7 +506,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                     s_point[r] = pt;
                     s_rpos[r] = rp;
                     s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)(owner * 16 + u);
-                    if constexpr (PIPE) s_apos[r * WIN + (t & (WIN - 1))] = (uint16_t)emb_off(owner * 16 + u, 0);
+                    if constexpr (PIPE) s_apos[apos_at(r, t)] = (uint16_t)emb_off(owner * 16 + u, 0);
                 }
                 if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
                 if (last1[n]) {
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                     for (int k = 0; k < 4; ++k) {
                         const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - s_start[r];
                         if (pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
-                        if constexpr (PIPE) s_apos[r * WIN + 4 * u + k] = (uint16_t)emb_off(SOS, 0);
+                        if constexpr (PIPE) s_apos[apos_at(r, 4 * u + k)] = (uint16_t)emb_off(SOS, 0);
                     }
                     if (u == 0) {
                         status[c] = s_stat[r];
