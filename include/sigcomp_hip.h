@@ -86,7 +86,7 @@ const uint64_t *sc_model_lut(const sc_model *model);
 /* MLP core the model runs on: 2 = pipelined core with per-tensor requant
  * (every layer's constants satisfy m0 < 2**31 and shift >= 32 after the
  * m0 = 2**31 rewrite, ReLU on every layer but the last, and one m0 and
- * shift per layer on all but the last, as in both bundled checkpoints;
+ * shift per layer, as in both bundled checkpoints;
  * tiles of up to 128 rows; every kernel), 1 = pipelined core with
  * per-channel constants (the explicit-context kernels; compress and
  * decompress run the plain core), 0 = plain core (any valid model; also

@@ -53,7 +53,8 @@ struct LayerDev {
     int32_t fast;            // every m0 < 2**31 and shift >= 32; shift[] holds shift - 32
     int32_t uni;             // fast, and one m0 and shift for every output (per-tensor constants):
     int32_t um0, ush;        //   that m0 and shift - 32
-    int32_t uhi;             //   the pre-shift clamp bound min(128 * 2**ush - 1, 2**31 - 1)
+    int32_t uhi;             //   the pre-shift clamp bounds min(128 * 2**ush - 1, 2**31 - 1)
+    int32_t ulo;             //   and max(-128 * 2**ush, -2**31) (layers without ReLU)
 };
 
 struct ModelDev {
@@ -66,8 +67,9 @@ struct ModelDev {
 
 // MLP cores.  CORE_PIPE (sc_pipe.h) needs every layer fast with ReLU on all
 // but the last; CORE_PIPE_UNI additionally per-tensor constants on every
-// layer but the last (their requantisation then takes four VALU
-// instructions per value, rq_word_uni).  All three give identical results.
+// layer (their requantisation then takes four VALU instructions per value,
+// rq_words_uni, and the LDS parameter slots hold only biases).  All three
+// give identical results.
 constexpr int CORE_PLAIN = 0, CORE_PIPE = 1, CORE_PIPE_UNI = 2;
 
 // ---------------------------------------------------------------- LDS layouts

@@ -39,12 +39,14 @@ __device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb
     else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, apos, wave, lane);
 }
 // once per kernel, before the first mlp_tile (and a barrier)
-template <bool PIPE>
+template <int CORE>
 __device__ __forceinline__ void mlp_tile_init(const ModelDev &M, uint32_t *s_par, int wave, int lane) {
-    if constexpr (PIPE) pipe_params_init(M, s_par, wave, lane);
+    if constexpr (CORE != CORE_PLAIN) pipe_params_init<CORE == CORE_PIPE_UNI>(M, s_par, wave, lane);
 }
-template <bool PIPE>
-constexpr int par_lds_dwords() { return PIPE ? PIPE_PAR_DWORDS : PAR_LDS_DWORDS; }
+template <int CORE>
+constexpr int par_lds_dwords() {
+    return CORE == CORE_PLAIN ? PAR_LDS_DWORDS : pipe_par_dwords<CORE == CORE_PIPE_UNI>();
+}
 // activation row layout of the core: padded rows (pipelined) or swizzled rows
 template <bool PIPE>
 constexpr int act_row_bytes() { return PIPE ? PACT_ROW : ACT_ROW; }
@@ -64,13 +66,13 @@ __global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const in
     // one LDS bank
     constexpr int CTX_STRIDE = WIN + 2;
     __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * CTX_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
     __shared__ double s_lut[VOCAB];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    mlp_tile_init<PIPE>(M, s_par, wave, lane);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
     const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
     // A tile's 128 x 64 context tokens: 32 per thread, all loads issued
     // before the first is used (a load / wait / store loop costs one memory
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     static_assert((R_TILE / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must stay inside the tile");
     __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
     __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
     __shared__ uint16_t s_tok[R_TILE + WIN];
     __shared__ uint16_t s_apos[R_TILE + WIN];   // emb_off(s_tok[i], 0)
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     const int q4 = lane >> 4, u = lane & 15;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    mlp_tile_init<PIPE>(M, s_par, wave, lane);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
     static_assert(R_TILE + WIN <= THREADS, "one staged token per thread");
     const int32_t n_tiles = (int32_t)min<int64_t>(tile_start[n_chunks], max_desc);
     // The next tile's descriptor is loaded during this tile's epilogue.
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     __shared__ __attribute__((aligned(16))) uint16_t s_apos[PIPE ? R * WIN : 1];
     auto apos_at = [](int r, int32_t pos) { return (pos & (WIN - 1)) * R + r; };
     __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
-    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
     __shared__ double s_lut[VOCAB];
     __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
     __shared__ int64_t s_woff[R], s_toff[R];
@@ -418,7 +420,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     if (t_begin > 0 && t_begin >= t_stop) return;
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    mlp_tile_init<PIPE>(M, s_par, wave, lane);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
     __syncthreads();
     if (t_begin > 0) {
         // the context ring: the 64 tokens before t_begin, already written to
@@ -1021,6 +1023,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         D.um0 = uni ? (int32_t)m0[0] : 0;
         D.ush = uni ? sh[0] : 0;
         D.uhi = uni ? (int32_t)std::min<int64_t>((int64_t(128) << sh[0]) - 1, INT32_MAX) : 0;
+        D.ulo = uni ? (int32_t)std::max<int64_t>(-(int64_t(128) << sh[0]), INT32_MIN) : 0;
         std::vector<uint32_t> par((size_t)(L.n / 32) * PAR_DWORDS, 0u);
         for (int nt = 0; nt < L.n / 32; ++nt) {
             uint32_t *blk = par.data() + (size_t)nt * PAR_DWORDS;
@@ -1044,7 +1047,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     bool pipe = !(plain && plain[0] == '1'), uni = true;
     for (int i = 0; i < n_layers; ++i) {
         if (!m->dev.layer[i].fast || m->dev.layer[i].relu != (i < n_layers - 1 ? 1 : 0)) pipe = false;
-        if (i < n_layers - 1 && !m->dev.layer[i].uni) uni = false;
+        if (!m->dev.layer[i].uni) uni = false;
     }
     m->dev.pipe = !pipe ? CORE_PLAIN : uni ? CORE_PIPE_UNI : CORE_PIPE;
     if (rc != SC_OK) {

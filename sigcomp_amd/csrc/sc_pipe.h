@@ -33,8 +33,16 @@ namespace sc {
 
 constexpr int PNT = 2;                               // n-tiles per pass
 constexpr int PPD = 4;                               // weight prefetch distance (k-steps)
-constexpr int PBLK = PNT * PAR_DWORDS;               // parameter dwords of one pass
-constexpr int PBLK_LANE = (PBLK + 63) / 64;
+// Parameter slot geometry.  The per-channel core keeps whole parameter
+// blocks (bias, m0, shift) in its slots; the per-tensor core (UNI) only the
+// bias of each n-tile, its m0, shift and clamp bounds being per-layer
+// scalars (7.7 KB less LDS).
+template <bool UNI>
+struct Slot {
+    static constexpr int TD = UNI ? 32 : PAR_DWORDS;   // dwords per n-tile
+    static constexpr int BLK = PNT * TD;               // parameter dwords of one pass
+    static constexpr int LANE = (BLK + 63) / 64;       // of them per lane when copied
+};
 // LDS parameter slots per wave: slot_p0(l) holds the pass-0 parameter blocks
 // of layer l, slot_p1(l) its pass-1 blocks.  Layers l >= 1 use four slots by
 // parity: layer l's pass-0 blocks are written during layer l-1 (layer l's
@@ -43,7 +51,8 @@ constexpr int PBLK_LANE = (PBLK + 63) / 64;
 // slots are written once per kernel (pipe_params_init), before the first MLP
 // evaluation, so that its bias tiles are in LDS when each evaluation starts.
 constexpr int PIPE_SLOTS = 6;
-constexpr int PIPE_PAR_DWORDS = WAVES * PIPE_SLOTS * PBLK;
+template <bool UNI>
+constexpr int pipe_par_dwords() { return WAVES * PIPE_SLOTS * Slot<UNI>::BLK; }
 __device__ __forceinline__ int slot_p0(int l) { return l == 0 ? 4 : (l & 1); }
 __device__ __forceinline__ int slot_p1(int l) { return l == 0 ? 5 : 2 + (l & 1); }
 
@@ -52,8 +61,9 @@ __device__ __forceinline__ int slot_p1(int l) { return l == 0 ? 5 : 2 + (l & 1);
 // the feature that accumulator element holds.  A GEMM whose first MFMA
 // accumulates onto it ends with acc + bias (int32, wrapping like the
 // reference's add), so the requantisation skips the bias add.
+template <bool UNI>
 __device__ __forceinline__ v16i bias_tile(const uint32_t *blk, int j, int g) {
-    const uint32_t *pj = blk + j * PAR_DWORDS + 4 * g;
+    const uint32_t *pj = blk + j * Slot<UNI>::TD + 4 * g;
     v16i t;
 #pragma unroll
     for (int gg = 0; gg < 4; ++gg) {
@@ -101,44 +111,79 @@ __device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar 
 // then writes each byte straight into the packed word (SDWA destination
 // select; byte 0 clears the others).  Four VALU instructions per value with
 // the accumulator read, and no per-channel operands.
+// Without ReLU (the output layer) the clamp is to [ulo, uhi], ulo =
+// -128 * 2**sh (or -2**31), and the shift is arithmetic.
 struct RqUni {
-    int m0, hi, sh;
+    int m0, hi, sh, lo;
 };
 __device__ __forceinline__ RqUni rq_uni(const LayerDev &L) {
     return RqUni{__builtin_amdgcn_readfirstlane(L.um0), __builtin_amdgcn_readfirstlane(L.uhi),
-                 __builtin_amdgcn_readfirstlane(L.ush)};
+                 __builtin_amdgcn_readfirstlane(L.ush), __builtin_amdgcn_readfirstlane(L.ulo)};
 }
-template <int E>
+template <bool RELU, int E>
 __device__ __forceinline__ void rq_insert_uni(uint32_t &packed, int sh, int y) {
-    if constexpr (E == 0)
-        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
-            : "=v"(packed) : "v"(sh), "v"(y));
-    else if constexpr (E == 1)
-        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-            : "+v"(packed) : "v"(sh), "v"(y));
-    else if constexpr (E == 2)
-        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-            : "+v"(packed) : "v"(sh), "v"(y));
-    else
-        asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-            : "+v"(packed) : "v"(sh), "v"(y));
+    if constexpr (RELU) {   // y >= 0
+        if constexpr (E == 0)
+            asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+                : "=v"(packed) : "v"(sh), "v"(y));
+        else if constexpr (E == 1)
+            asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+        else if constexpr (E == 2)
+            asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+        else
+            asm("v_lshrrev_b32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+    } else {
+        if constexpr (E == 0)
+            asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+                : "=v"(packed) : "v"(sh), "v"(y));
+        else if constexpr (E == 1)
+            asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+        else if constexpr (E == 2)
+            asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+        else
+            asm("v_ashrrev_i32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+                : "+v"(packed) : "v"(sh), "v"(y));
+    }
 }
 // Features 8g + 4*g2 + e (e = 0..3) of accumulator tiles acc[i], I0 <= i <
 // I1 -> packed words pk[i][g].  The inserts run byte by byte across the
 // words, so that consecutive inserts write different registers.
-template <int I0, int I1, int RT>
+template <bool RELU, int I0, int I1, int RT>
 __device__ __forceinline__ void rq_words_uni(const v16i (&acc)[RT], int g, const RqUni &p, uint32_t (&pk)[RT][4]) {
     int y[4][RT];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int i = I0; i < I1; ++i)
-            asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "s"(p.hi));
+        for (int i = I0; i < I1; ++i) {
+            if constexpr (RELU)
+                asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "s"(p.hi));
+            else
+                asm("v_med3_i32 %0, %1, %2, %3"
+                    : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "v"(p.lo), "s"(p.hi));
+        }
     static_for<4>([&](auto ec) __attribute__((always_inline)) {
         constexpr int e = decltype(ec)::value;
 #pragma unroll
-        for (int i = I0; i < I1; ++i) rq_insert_uni<e>(pk[i][g], p.sh, y[e][i]);
+        for (int i = I0; i < I1; ++i) rq_insert_uni<RELU, e>(pk[i][g], p.sh, y[e][i]);
     });
+}
+// All n-tiles and row tiles of a pass (the requantisations that are not
+// interleaved with MFMAs: layer 0's pass 0 and the output layer).
+template <bool RELU, int RT>
+__device__ __forceinline__ void rq_pass_uni(const v16i (&acc)[PNT][RT], const RqUni &p, uint32_t (&pk)[PNT][RT][4]) {
+#pragma unroll
+    for (int j = 0; j < PNT; ++j)
+        static_for<4>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value;
+            rq_words_uni<RELU, 0, RT>(acc[j], g, p, pk[j]);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) asm volatile("" : "+v"(pk[j][i][g]));
+        });
 }
 
 __device__ __forceinline__ v4i wload_s(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
@@ -152,28 +197,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t layer_rsrc(const LayerDev &L) 
 }
 
 // Parameter blocks of one pass (n-tiles nt0, nt0 + 1) into registers / LDS.
-__device__ __forceinline__ void par_fetch(const uint32_t *gpar, int nt0, int lane, uint32_t (&pr)[PBLK_LANE]) {
+// (the first Slot<UNI>::TD dwords of each n-tile's block)
+template <bool UNI>
+__device__ __forceinline__ void par_fetch(const uint32_t *gpar, int nt0, int lane, uint32_t (&pr)[Slot<UNI>::LANE]) {
+    using S = Slot<UNI>;
 #pragma unroll
-    for (int d = 0; d < PBLK_LANE; ++d) {
+    for (int d = 0; d < S::LANE; ++d) {
         const int idx = d * 64 + lane;
-        pr[d] = idx < PBLK ? gpar[nt0 * PAR_DWORDS + idx] : 0u;
+        pr[d] = idx < S::BLK ? gpar[(nt0 + idx / S::TD) * PAR_DWORDS + idx % S::TD] : 0u;
     }
 }
-__device__ __forceinline__ void par_put(uint32_t *blk, const uint32_t (&pr)[PBLK_LANE], int lane) {
+template <bool UNI>
+__device__ __forceinline__ void par_put(uint32_t *blk, const uint32_t (&pr)[Slot<UNI>::LANE], int lane) {
 #pragma unroll
-    for (int d = 0; d < PBLK_LANE; ++d)
-        if (d * 64 + lane < PBLK) blk[d * 64 + lane] = pr[d];
+    for (int d = 0; d < Slot<UNI>::LANE; ++d)
+        if (d * 64 + lane < Slot<UNI>::BLK) blk[d * 64 + lane] = pr[d];
 }
 
 // Layer 0's parameter blocks (read by every MLP evaluation of the kernel)
 // into their slots; the caller's next barrier makes them visible.
+template <bool UNI>
 __device__ __forceinline__ void pipe_params_init(const ModelDev &M, uint32_t *s_par, int wave, int lane) {
-    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * PBLK;
-    uint32_t pr[PBLK_LANE];
-    par_fetch(M.layer[0].par, 2 * wave, lane, pr);
-    par_put(s_parw + slot_p0(0) * PBLK, pr, lane);
-    par_fetch(M.layer[0].par, 8 + 2 * wave, lane, pr);
-    par_put(s_parw + slot_p1(0) * PBLK, pr, lane);
+    constexpr int BLK = Slot<UNI>::BLK;
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
+    uint32_t pr[Slot<UNI>::LANE];
+    par_fetch<UNI>(M.layer[0].par, 2 * wave, lane, pr);
+    par_put<UNI>(s_parw + slot_p0(0) * BLK, pr, lane);
+    par_fetch<UNI>(M.layer[0].par, 8 + 2 * wave, lane, pr);
+    par_put<UNI>(s_parw + slot_p1(0) * BLK, pr, lane);
 }
 
 // Activation rows of the pipelined core are padded to PACT_ROW bytes instead
@@ -252,14 +303,15 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     const __amdgpu_buffer_rsrc_t rs = layer_rsrc(L);
     const __amdgpu_buffer_rsrc_t rsn = layer_rsrc(Ln);
     const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;   // n-tile bases of pass 0 / pass 1
-    const uint32_t *prev1 = s_parw + slot_p1(l - 1) * PBLK;
-    const uint32_t *cur0 = s_parw + slot_p0(l) * PBLK;
-    uint32_t *cur1 = s_parw + slot_p1(l) * PBLK;
-    uint32_t *next0 = s_parw + slot_p0(l + 1) * PBLK;
-    uint32_t pr1[PBLK_LANE], prn[PBLK_LANE];
+    constexpr int BLK = Slot<UNI>::BLK;
+    const uint32_t *prev1 = s_parw + slot_p1(l - 1) * BLK;
+    const uint32_t *cur0 = s_parw + slot_p0(l) * BLK;
+    uint32_t *cur1 = s_parw + slot_p1(l) * BLK;
+    uint32_t *next0 = s_parw + slot_p0(l + 1) * BLK;
+    uint32_t pr1[Slot<UNI>::LANE], prn[Slot<UNI>::LANE];
     if constexpr (!LASTL) {
-        par_fetch(L.par, nb1, lane, pr1);
-        par_fetch(Ln.par, nb0, lane, prn);
+        par_fetch<UNI>(L.par, nb1, lane, pr1);
+        par_fetch<UNI>(Ln.par, nb0, lane, prn);
     }
     v4i b[2][RT];
     read_b<RT>(s_act, bbase, 0, b[0]);
@@ -272,7 +324,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     }
     v16i bias[PNT];
 #pragma unroll
-    for (int j = 0; j < PNT; ++j) bias[j] = bias_tile(cur0, j, g);
+    for (int j = 0; j < PNT; ++j) bias[j] = bias_tile<UNI>(cur0, j, g);
     static_for<NV>([&](auto vc) __attribute__((always_inline)) {
         constexpr int v = decltype(vc)::value;
         constexpr int pass = v / KTH, kt = v % KTH, set = (v / PPD) & 1, slot = v % PPD;
@@ -296,7 +348,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         if constexpr (v < 8) {
             constexpr int j = v / 4, gg = v % 4;
             if constexpr (UNI) {
-                rq_words_uni<0, RT>(accB[j], gg, up, pk[j]);
+                rq_words_uni<true, 0, RT>(accB[j], gg, up, pk[j]);
             } else {
                 const RqPar cur = pp;
                 if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
@@ -306,7 +358,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         } else if constexpr (!LASTL && v >= 16) {
             constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
             if constexpr (UNI) {
-                rq_words_uni<h * RH, (h ? RT : RH)>(accA[j], gg, uc, pk[j]);
+                rq_words_uni<true, h * RH, (h ? RT : RH)>(accA[j], gg, uc, pk[j]);
             } else {
                 const RqPar cur = pp;
                 if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
@@ -317,7 +369,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         // pass 1's bias tiles, one step before its first MFMAs
         if constexpr (!LASTL && v == KTH - 1) {
 #pragma unroll
-            for (int j = 0; j < PNT; ++j) bias[j] = bias_tile(cur1, j, g);
+            for (int j = 0; j < PNT; ++j) bias[j] = bias_tile<UNI>(cur1, j, g);
         }
         // this step's MFMAs
         auto &acc = pass == 0 ? accA : accB;
@@ -334,8 +386,8 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
             // layer's pass-0 parameters -> LDS
             pstore_perm<RT>(pk, nb1, s_act, lane);
             if constexpr (!LASTL) {
-                par_put(cur1, pr1, lane);
-                par_put(next0, prn, lane);
+                par_put<UNI>(cur1, pr1, lane);
+                par_put<UNI>(next0, prn, lane);
                 if constexpr (!UNI) pp = rq_par(cur0, 0, 0, g);   // first parameters of the pass-0 requantisation
             }
             __syncthreads();
@@ -343,7 +395,8 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         }
     });
     if constexpr (LASTL) {
-        requant_pack_t<PNT, RT, true, false, false>(accA, cur0, lane, pk);
+        if constexpr (UNI) rq_pass_uni<false, RT>(accA, rq_uni(L), pk);
+        else requant_pack_t<PNT, RT, true, false, false>(accA, cur0, lane, pk);
         __syncthreads();
         pstore_natural<RT>(pk, nb0, s_act, lane);
     } else {
@@ -356,7 +409,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
 // One MLP evaluation of R = 32*RT rows (RT <= 4), same contract as mlp_rows
 // but in the padded row layout: entered after a barrier that ends every read
 // of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of
-// each row (natural order) after a barrier.  s_par holds PIPE_PAR_DWORDS,
+// each row (natural order) after a barrier.  s_par holds pipe_par_dwords<UNI>(),
 // layer 0's slots filled by pipe_params_init.
 template <int RT, bool UNI, class AposFn>
 __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
@@ -368,7 +421,8 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     wave = __builtin_amdgcn_readfirstlane(wave);
     const int voff = lane * 16;
     const int nb0 = 2 * wave, nb1 = 8 + 2 * wave;
-    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * PBLK;
+    constexpr int BLK = Slot<UNI>::BLK;
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
     v16i accA[PNT][RT], accB[PNT][RT];
     v4i w[2][PPD][PNT];
     uint32_t pk[PNT][RT][4];
@@ -380,22 +434,23 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     {
         const LayerDev &L0 = M.layer[0];
         const int g = lane >> 5;
-        const uint32_t *p00 = s_parw + slot_p0(0) * PBLK, *p10 = s_parw + slot_p1(0) * PBLK;
-        uint32_t prn[PBLK_LANE];
-        par_fetch(M.layer[1].par, nb0, lane, prn);
+        const uint32_t *p00 = s_parw + slot_p0(0) * BLK, *p10 = s_parw + slot_p1(0) * BLK;
+        uint32_t prn[Slot<UNI>::LANE];
+        par_fetch<UNI>(M.layer[1].par, nb0, lane, prn);
         v16i bias[2 * PNT];
 #pragma unroll
         for (int j = 0; j < PNT; ++j) {
-            bias[j] = bias_tile(p00, j, g);
-            bias[PNT + j] = bias_tile(p10, j, g);
+            bias[j] = bias_tile<UNI>(p00, j, g);
+            bias[PNT + j] = bias_tile<UNI>(p10, j, g);
         }
         const WStream ws = make_wstream(L0.w, L0.bytes);
         gemm_layer0_map<2 * PNT, RT>(
             ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, apos,
             [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; },
             [&](int j, int) { return bias[j]; }, lane);
-        par_put(s_parw + slot_p0(1) * PBLK, prn, lane);
-        requant_pack_t<PNT, RT, true, true, false>(accA, p00, lane, pk);
+        par_put<UNI>(s_parw + slot_p0(1) * BLK, prn, lane);
+        if constexpr (UNI) rq_pass_uni<true, RT>(accA, rq_uni(L0), pk);
+        else requant_pack_t<PNT, RT, true, true, false>(accA, p00, lane, pk);
         pstore_perm<RT>(pk, nb0, s_act, lane);
         const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
 #pragma unroll

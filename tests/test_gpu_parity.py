@@ -221,6 +221,21 @@ def test_compress_decompress_chunks_match_oracle(codecs, oracle_mod, oracle_mode
         assert np.array_equal(c, b)
 
 
+def test_compress_tile_table_with_empty_chunks(codecs, oracle_mod, oracle_models):
+    """Compress finds each 128-step tile through a descriptor table built
+    from the tile offsets of the chunks; empty chunks own no tiles and share
+    their offset with the next chunk.  Empty chunks between, before and after
+    chunks whose lengths end on and just past tile boundaries."""
+    lengths = [0, 5, 0, 0, 128, 129, 0, 256, 1, 0]
+    rng = np.random.default_rng(31)
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    gpu = codecs["lossless"].compress_chunks(chunks)
+    assert gpu == oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    assert [len(b) == 0 for b in gpu] == [n == 0 for n in lengths]
+    back = codecs["lossless"].decompress_chunks(gpu, lengths)
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+
+
 def test_decompress_many_chunks_round_trip(codecs):
     """More chunks than one workgroup row tile per CU; mixed lengths."""
     rng = np.random.default_rng(11)
@@ -328,25 +343,27 @@ def test_fast_requant_clamp_bounds_match_oracle(oracle_mod, monkeypatch, core):
     assert np.array_equal(got, exp)
 
 
-@pytest.mark.parametrize("shift", [32, 33, 38, 56, 63])
-def test_per_tensor_requant_matches_oracle(oracle_mod, shift):
+@pytest.mark.parametrize("layer,shift", [(2, 32), (2, 33), (2, 38), (2, 56), (2, 63),
+                                         (-1, 32), (-1, 38), (-1, 56), (-1, 63)])
+def test_per_tensor_requant_matches_oracle(oracle_mod, layer, shift):
     """Per-tensor constants (one m0 and shift per layer, as in the bundled
-    checkpoints) select core 2, whose hidden-layer requantisation clamps
-    before the shift against a per-layer bound and shifts into the packed
-    byte.  Layer 2's shift: 32 (most values saturate at 127), 33, 38, 56
-    (the bound 128 * 2**24 - 1 exceeds int32 and is capped) and 63; layer 0
-    (requantised by both paths: pass 0 per channel, pass 1 per tensor) keeps
-    its drawn constants.  Logits, CDFs, chunk bytes and the round trip are
-    compared with the oracle."""
+    checkpoints) select core 2, whose requantisation clamps before the shift
+    against per-layer bounds and shifts into the packed byte.  Layer 2's
+    shift: 32 (most values saturate at 127), 33, 38, 56 (the bound
+    128 * 2**24 - 1 exceeds int32 and is capped) and 63; the output layer's
+    (no ReLU, arithmetic shift): 32 (saturation at -128 and 127), 38, 56
+    (both bounds capped) and 63.  Logits, CDFs, chunk bytes and the round
+    trip are compared with the oracle."""
     import dataclasses
     from sigcomp_amd.model_io import make_layer, random_int_model
     from sigcomp_amd.quant_mlp_export import QuantMLPCompression
     m = random_int_model(seed=17, per_channel=False)
     rng = np.random.default_rng(17)
     layers = list(m.layers)
-    L = layers[2]
+    li = layer % len(layers)
+    L = layers[li]
     m0 = int(rng.integers(1 << 30, 1 << 31))
-    layers[2] = make_layer(L.weight, L.bias, np.full(L.n, m0), np.full(L.n, shift, np.int32), True)
+    layers[li] = make_layer(L.weight, L.bias, np.full(L.n, m0), np.full(L.n, shift, np.int32), L.relu)
     model = dataclasses.replace(m, layers=layers)
     codec = QuantMLPCompression(chunk_len=2048, gpu=0, model=model)
     assert codec.hip.core == 2
@@ -354,6 +371,8 @@ def test_per_tensor_requant_matches_oracle(oracle_mod, shift):
     ctx = rng.integers(0, 257, (300, 64))
     ctx[:40, :25] = 256
     exp = oracle_mod.mlp_forward(om, ctx)
+    if li == len(layers) - 1 and shift == 32:
+        assert (exp == 127).any() and (exp == -128).any()
     got = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
     assert np.array_equal(got, exp)
     cdf = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "cdf").cpu().numpy()

@@ -50,3 +50,17 @@ def test_clamp_before_shift_identity():
         edges = [hi - 1, hi, hi + 1, 127 * 2**sh - 1, 127 * 2**sh, 128 * 2**sh]
         for x in xs + [e for e in edges if -(2**31) <= e < 2**31]:
             assert min(max(x >> sh, 0), 127) == (min(max(x, 0), hi) >> sh)
+
+
+def test_signed_clamp_before_shift_identity():
+    """Output layer (no ReLU) with per-tensor constants: x clamped to
+    [lo, hi] and shifted arithmetically by sh equals the clamp of x >> sh to
+    [-128, 127], with lo = -128 * 2**sh capped at -2**31 and hi as above."""
+    rng = np.random.default_rng(3)
+    xs = [-(2**31), -(2**31) + 1, -1, 0, 1, 2**31 - 1] + [int(v) for v in rng.integers(-2**31, 2**31, 4000)]
+    for sh in range(32):
+        hi = min(128 * 2**sh - 1, 2**31 - 1)
+        lo = max(-128 * 2**sh, -(2**31))
+        edges = [lo - 1, lo, lo + 1, hi - 1, hi, hi + 1, -127 * 2**sh, -127 * 2**sh - 1]
+        for x in xs + [e for e in edges if -(2**31) <= e < 2**31]:
+            assert min(max(x >> sh, -128), 127) == (min(max(x, lo), hi) >> sh)
