@@ -21,8 +21,10 @@
 //   boundaries.  Accumulators of the two passes take 2 x 2 x RT x 16 AGPRs
 //   (256 for RT = 4).
 //
-// With UNI (CORE_PIPE_UNI: per-tensor constants on every layer but the
-// last) the interleaved requantisation is rq_words_uni, else rq_word.
+// With UNI (CORE_PIPE_UNI: per-tensor constants on every layer) every
+// requantisation is rq_words_uni / rq_pass_uni and the parameter slots hold
+// only biases; else the hidden layers use rq_word, layer 0's first pass and
+// the output layer requant_pack_t.
 // Requires every layer to take the 32-bit requant path (LayerDev::fast), ReLU
 // on all layers but the last, and 512-wide hidden layers (ModelDev::pipe).
 #pragma once
