@@ -34,7 +34,11 @@
 namespace sc {
 
 constexpr int PNT = 2;                               // n-tiles per pass
-constexpr int PPD = 4;                               // weight prefetch distance (k-steps)
+// Weight prefetch distance in k-steps: 8 where the registers allow (tiles
+// of up to 96 rows), else 4.  Both divide the 16 and 32 k-steps of a pass,
+// as the two-set register rotation needs.
+template <int RT>
+constexpr int ppd() { return RT <= 3 ? 8 : 4; }
 // Parameter slot geometry.  The per-channel core keeps whole parameter
 // blocks (bias, m0, shift) in its slots; the per-tensor core (UNI) only the
 // bias of each n-tile, its m0, shift and clamp bounds being per-layer
@@ -295,8 +299,9 @@ __device__ __forceinline__ void pipe_schedule() {
 template <int RT, bool LASTL, bool UNI>
 __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
                                             uint32_t *s_parw, int l, v16i (&accA)[PNT][RT],
-                                            v16i (&accB)[PNT][RT], v4i (&w)[2][PPD][PNT],
+                                            v16i (&accB)[PNT][RT], v4i (&w)[2][ppd<RT>()][PNT],
                                             uint32_t (&pk)[PNT][RT][4], int wave, int lane) {
+    constexpr int PPD = ppd<RT>();
     constexpr int NV = LASTL ? KTH : 2 * KTH;
     constexpr int MF = PNT * RT;
     constexpr int RH = (RT + 1) / 2;          // row tiles requantised in the first of two steps
@@ -426,6 +431,7 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
     constexpr int BLK = Slot<UNI>::BLK;
     uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
     v16i accA[PNT][RT], accB[PNT][RT];
+    constexpr int PPD = ppd<RT>();
     v4i w[2][PPD][PNT];
     uint32_t pk[PNT][RT][4];
     // layer 0 in one pass over both passes' n-tiles (each embedding B
