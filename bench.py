@@ -169,6 +169,16 @@ def bench_codec(args):
                      "traffic_source": f"profiles/traffic_{args.config}.txt (rocprofv3 PMC, bytes per launch)",
                      "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch",
                      **ceiling_fields(achieved), **pmc_mfma(args.config, "k_decompress")},
+        # the other half of the round trip, same fields (the compress call:
+        # k_tile_scan, k_tile_table, k_compress_mlp, k_encode_pairs)
+        "roofline_compress": {"kernel": "k_compress_mlp", "bound": "mfma",
+                              "achieved": round(rows * OPS_PER_ROW / t_c / 1e12, 2), "peak": PEAK_INT8_TOPS,
+                              "unit": "TFLOP/s",
+                              "frac": round(rows * OPS_PER_ROW / t_c / 1e12 / PEAK_INT8_TOPS, 4),
+                              "traffic": pmc_traffic(args.config, "k_compress_mlp"),
+                              "algorithmic": f"{OPS_PER_ROW} int8 ops per coded token x {rows} tokens per launch",
+                              **ceiling_fields(rows * OPS_PER_ROW / t_c / 1e12),
+                              **pmc_mfma(args.config, "k_compress_mlp")},
     }
     return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
 
