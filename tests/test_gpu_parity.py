@@ -236,6 +236,25 @@ def test_compress_tile_table_with_empty_chunks(codecs, oracle_mod, oracle_models
     assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
 
 
+def test_long_chunk_len_matches_oracle(int_models, oracle_mod, oracle_models):
+    """chunk_len 5000 (the reference lets the caller choose it): chunks span
+    40 compress tiles and 20 decode launches of 256 steps, lengths not on
+    tile or segment boundaries; then a read framed into such chunks."""
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    codec = QuantMLPCompression(chunk_len=5000, gpu=0, model=int_models["lossless"])
+    rng = np.random.default_rng(41)
+    lengths = [5000, 4999, 2049, 300]
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    gpu = codec.compress_chunks(chunks)
+    assert gpu == oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    back = codec.decompress_chunks(gpu, lengths)
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
+    read = rng.integers(0, 60, 12345).astype(np.uint8)
+    framed = codec.batch_inference_reads(list_of_reads=[read])
+    out = codec.batch_inference_reads(list_of_compressed_reads=framed, list_of_lengths=[read.size])
+    assert np.array_equal(out[0], read)
+
+
 def test_decompress_many_chunks_round_trip(codecs):
     """More chunks than one workgroup row tile per CU; mixed lengths."""
     rng = np.random.default_rng(11)
