@@ -149,7 +149,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_tile_scan(const int32_t *__res
     const int64_t per = (n_chunks + SCAN_THREADS - 1) / SCAN_THREADS;
     const int64_t c0 = threadIdx.x * per, c1 = min(c0 + per, n_chunks);
     int32_t sum = 0;
-    for (int64_t c = c0; c < c1; ++c) sum += (lengths[c] + R_TILE - 1) / R_TILE;
+    // a negative length counts as empty: offsets stay monotone and non-negative
+    for (int64_t c = c0; c < c1; ++c) sum += (max(lengths[c], 0) + R_TILE - 1) / R_TILE;
     s_sum[threadIdx.x] = sum;
     __syncthreads();
     for (int d = 1; d < SCAN_THREADS; d <<= 1) {
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_tile_scan(const int32_t *__res
     int32_t run = s_sum[threadIdx.x] - sum;
     for (int64_t c = c0; c < c1; ++c) {
         tile_start[c] = run;
-        run += (lengths[c] + R_TILE - 1) / R_TILE;
+        run += (max(lengths[c], 0) + R_TILE - 1) / R_TILE;
     }
     if (threadIdx.x == SCAN_THREADS - 1) tile_start[n_chunks] = s_sum[SCAN_THREADS - 1];
 }

@@ -236,6 +236,38 @@ def test_compress_tile_table_with_empty_chunks(codecs, oracle_mod, oracle_models
     assert all(np.array_equal(a, b) for a, b in zip(chunks, back))
 
 
+def test_compress_abi_negative_length_owns_no_tiles(codecs, oracle_mod, oracle_models):
+    """Through the C ABI (the Python layer rejects it), a negative chunk
+    length counts as an empty chunk: it owns no compress tiles and no words,
+    and the other chunks' tiles and bytes are unaffected."""
+    from sigcomp_amd import _hip
+    codec = codecs["lossless"]
+    rng = np.random.default_rng(43)
+    lengths = np.array([5, -300, 130, 0, 257], np.int32)
+    used = np.maximum(lengths, 0)
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in used]
+    n = len(lengths)
+    n_tokens = int(used.sum())
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(used[:-1], out=tok_off[1:])
+    cap = (used + 2).astype(np.int32)
+    word_off = np.zeros(n, np.int64)
+    np.cumsum(cap[:-1].astype(np.int64), out=word_off[1:])
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_tok, t_off, t_len, t_woff, t_cap = d(np.concatenate(chunks)), d(tok_off), d(lengths), d(word_off), d(cap)
+    words, cnt, status, ws = codec._compress_buffers(n, n_tokens, int(cap.sum()))
+    L, p = _hip.lib(), _hip.ptr
+    _hip.check(L.sc_compress_chunks(codec.hip.handle, p(t_tok), p(t_off), p(t_len), n, n_tokens, p(words),
+                                    p(t_woff), p(t_cap), p(cnt), p(status), p(ws), ws.numel(),
+                                    torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    w, c = words.cpu().numpy().view(np.uint32), cnt.cpu().numpy()
+    assert not status.cpu().numpy().any() and c[1] == 0
+    for i in range(n):
+        assert w[word_off[i]:word_off[i] + c[i]].tobytes() == ref[i]
+
+
 def test_long_chunk_len_matches_oracle(int_models, oracle_mod, oracle_models):
     """chunk_len 5000 (the reference lets the caller choose it): chunks span
     40 compress tiles and 20 decode launches of 256 steps, lengths not on
