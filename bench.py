@@ -97,11 +97,15 @@ def bench_codec(args):
                                         _hip.ptr(cnt), _hip.ptr(status), _hip.ptr(ws), ws.numel(),
                                         stream.cuda_stream))
 
+    o_len_host = np.ascontiguousarray(lengths[order])
+    dws = codec._decompress_workspace(n)
+
     def decompress():
         torch.index_select(cnt, 0, o_idx, out=o_cnt)
         _hip.check(L.sc_decompress_chunks(h, _hip.ptr(words), _hip.ptr(o_woff), _hip.ptr(o_cnt),
                                           _hip.ptr(o_len), n, _hip.ptr(out_tokens), _hip.ptr(o_toff),
-                                          _hip.ptr(dstatus), stream.cuda_stream))
+                                          _hip.ptr(dstatus), o_len_host.ctypes.data, _hip.ptr(dws),
+                                          dws.numel(), stream.cuda_stream))
 
     if args.copy_mib:
         # one plain elementwise kernel moving a known number of bytes (read

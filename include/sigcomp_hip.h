@@ -13,15 +13,18 @@
  *    (the library never frees caller memory).  "host" pointers are read during
  *    the call only.
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
- *    work is stream-ordered; no call synchronises the device.
+ *    work is stream-ordered; no call waits for the device, except
+ *    sc_decompress_chunks when it is not given the lengths on the host.
  *  - Return value: SC_OK or an SC_ERR_* code for argument / HIP errors found
  *    at launch time; sc_last_error() describes the last failure of the calling
  *    thread.  Data-dependent failures (an out-of-range token, an encoder
  *    capacity overflow, an invalid range stream) are reported through the
  *    caller's device `status` arrays with the SC_STATUS_* codes, since they
  *    are known only after the kernels ran.
- *  - One model handle may be used from several streams; calls that share a
- *    workspace or state arrays must not overlap.
+ *  - A model handle is read-only after sc_model_create: calls on several
+ *    streams or host threads may share it.  Each call's mutable device state
+ *    lives in memory the caller passes (workspace, state and output arrays);
+ *    calls that share such memory must not overlap.
  *
  * Architecture supported by the kernels: window 64, embedding 257 x 128,
  * layer 0 8192 -> 512, n_layers - 2 hidden layers 512 -> 512, last layer
@@ -197,27 +200,36 @@ int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_
  * limit for that operand data (the practical ceiling of the MLP kernels). */
 int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t *out, void *stream);
 
+/* Bytes of device workspace sc_decompress_chunks needs for n_chunks chunks:
+ * the coder state of every chunk between step segments (40 bytes per chunk)
+ * and the launch plan's four length statistics, each 256-byte aligned. */
+int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
+
 /* Decompress n_chunks chunks with persistent kernels: every workgroup owns a
  * tile of chunks and runs the autoregressive loop for them (MLP step, fused
  * frequency step and decoder step per token, context kept on chip), in
- * launches of 256 steps (the coder state of each chunk is carried between
- * them in a device buffer the model keeps and grows on demand; four chunk
- * length statistics are read back once per call for the launch plan, so the
- * call waits for the work already queued on `stream`).  Calls on one model
- * must not overlap (issue
- * them on one stream).  Chunk c: word_cnt[c] words at words + word_off[c] ->
- * lengths[c] tokens at tokens + tok_off[c]; status[c] is written
- * (SC_STATUS_INVALID_STREAM on a corrupt stream, whose tokens are then
- * unspecified).  All arrays device.  Chunks sorted by descending length (as
- * QuantMLPCompression passes them) give the shortest schedule: the shortest
- * chunks are then left over after the full waves of workgroups and follow
- * the shortest chunks of the last full wave in the same rows.  Replaces
- * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
- * (quant_mlp_export.py:325-377); output equals
+ * launches of 256 steps; the coder state of each chunk is carried between
+ * them in `workspace` (device, at least sc_decompress_workspace_bytes).
+ * Chunk c: word_cnt[c] words at words + word_off[c] -> lengths[c] tokens at
+ * tokens + tok_off[c]; status[c] is written (SC_STATUS_INVALID_STREAM on a
+ * corrupt stream, whose tokens are then unspecified).  Device arrays:
+ * words, word_off, word_cnt, lengths, tokens, tok_off, status, workspace.
+ * `lengths_host` is an optional host copy of `lengths` (the reference's
+ * list_of_lengths is host data): with it the launch plan is computed on the
+ * host and the call only enqueues work on `stream`; with NULL the plan's
+ * length statistics are computed on the device and read back, so the call
+ * waits for the work already queued on `stream`.  Chunks sorted by
+ * descending length (as QuantMLPCompression passes them) give the shortest
+ * schedule: the shortest chunks are then left over after the full waves of
+ * workgroups and follow the shortest chunks of the last full wave in the
+ * same rows.  Replaces QuantMLPCompression.decompress_chunks /
+ * _decompress_chunks_gpu (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */
 int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int64_t *word_off,
                          const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,
-                         uint8_t *tokens, const int64_t *tok_off, int32_t *status, void *stream);
+                         uint8_t *tokens, const int64_t *tok_off, int32_t *status,
+                         const int32_t *lengths_host, void *workspace, int64_t workspace_bytes,
+                         void *stream);
 
 #ifdef __cplusplus
 }

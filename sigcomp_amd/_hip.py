@@ -26,7 +26,7 @@ EXPORTED = (
     "sc_model_core",
     "sc_mlp_forward", "sc_mlp_forward_cdf", "sc_logits_to_cdf", "sc_encode_step",
     "sc_encode_seal", "sc_decode_step", "sc_compress_workspace_bytes", "sc_compress_chunks",
-    "sc_decompress_chunks", "sc_gather_words", "sc_mfma_burn_i8",
+    "sc_decompress_workspace_bytes", "sc_decompress_chunks", "sc_gather_words", "sc_mfma_burn_i8",
 )
 
 
@@ -87,13 +87,16 @@ def lib():
         L.sc_compress_workspace_bytes.restype = _I64
         L.sc_compress_chunks.argtypes = [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64,
                                          _P]
-        L.sc_decompress_chunks.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P]
+        L.sc_decompress_workspace_bytes.argtypes = [_I64]
+        L.sc_decompress_workspace_bytes.restype = _I64
+        L.sc_decompress_chunks.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P]
         L.sc_gather_words.argtypes = [_P, _P, _P, _I64, _P, _P, _P]
         L.sc_mfma_burn_i8.argtypes = [_P, _I32, _I32, _P, _P]
         for name in EXPORTED:
             fn = getattr(L, name)
             if fn.restype is None or fn.restype is ctypes.c_int:
-                if name not in ("sc_model_lut", "sc_compress_workspace_bytes"):
+                if name not in ("sc_model_lut", "sc_compress_workspace_bytes",
+                                "sc_decompress_workspace_bytes"):
                     fn.restype = ctypes.c_int
         _LIB = L
     return _LIB

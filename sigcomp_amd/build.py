@@ -14,18 +14,25 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 REPO = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libsigcomp_hip.so"
-SOURCES = [CSRC / "sc_kernels.hip"]
+# Translation units of libsigcomp_hip.so as (source, defines): the large MLP
+# kernels are split over several units so that they compile in parallel.
+UNITS = [(CSRC / "sc_kernels.hip", ()), (CSRC / "sc_comp.hip", ()),
+         (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=0",)), (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=1",)),
+         *[(CSRC / "sc_dec.hip", (f"SC_DEC_RT={rt}",)) for rt in range(1, 6)]]
+SOURCES = sorted({src for src, _ in UNITS})
 HOST_LIB = PKG / "libsigcomp_host.so"
 HOST_SOURCES = [CSRC / "sc_host.cpp"]
 HOST_FLAGS = ["-O3", "-march=x86-64-v3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra",
               f"-I{REPO / 'include'}"]
-HEADERS = [CSRC / "sc_device.h", REPO / "include" / "sigcomp_hip.h"]
+HEADERS = [CSRC / "sc_device.h", CSRC / "sc_pipe.h", CSRC / "sc_kernels.h", REPO / "include" / "sigcomp_hip.h"]
 ARCH = os.environ.get("SIGCOMP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -56,25 +63,54 @@ def build_host(verbose: bool = False) -> Path:
     return HOST_LIB
 
 
+def _unit_obj(tmp: Path, i: int, src: Path, defines) -> Path:
+    return tmp / f"{i:02d}_{src.stem}{''.join('_' + d.split('=')[-1] for d in defines)}.o"
+
+
 def build(verbose: bool = False, extra_flags=()) -> Path:
+    """Compile every translation unit (in parallel) and link the library."""
     build_host(verbose)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra_flags, *map(str, SOURCES), "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed for libsigcomp_hip.so")
-    os.replace(tmp, LIB)
+    with tempfile.TemporaryDirectory(prefix="sc_build_") as td:
+        tmp = Path(td)
+        compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        cmds = []
+        for i, (src, defines) in enumerate(UNITS):
+            obj = _unit_obj(tmp, i, src, defines)
+            cmds.append([hipcc(), *compile_flags, *extra_flags, *[f"-D{d}" for d in defines], "-c", str(src),
+                         "-o", str(obj)])
+        jobs = max(1, min(len(cmds), os.cpu_count() or 1, 16))
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            results = list(pool.map(lambda c: (c, subprocess.run(c, capture_output=True, text=True)), cmds))
+        for cmd, res in results:
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            if res.returncode != 0:
+                sys.stderr.write(res.stdout + res.stderr)
+                raise RuntimeError(f"hipcc failed for {cmd[-3]}")
+        out = LIB.with_suffix(".so.tmp")
+        link = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *extra_flags,
+                *[str(_unit_obj(tmp, i, s, d)) for i, (s, d) in enumerate(UNITS)], "-o", str(out)]
+        res = subprocess.run(link, capture_output=True, text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError("hipcc link failed for libsigcomp_hip.so")
+        os.replace(out, LIB)
     return LIB
 
 
 def device_asm(out_path: Path) -> Path:
-    """Write the gfx950 assembly of the library (for resource / ISA checks)."""
-    cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")],
-           "--cuda-device-only", "-S", *map(str, SOURCES), "-o", str(out_path)]
-    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    """Write the gfx950 assembly of every translation unit of the library,
+    concatenated (for resource / ISA checks)."""
+    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    with tempfile.TemporaryDirectory(prefix="sc_asm_") as td:
+        tmp = Path(td)
+        cmds = [[hipcc(), *flags, *[f"-D{d}" for d in defines], "--cuda-device-only", "-S", str(src), "-o",
+                 str(_unit_obj(tmp, i, src, defines).with_suffix(".s"))] for i, (src, defines) in enumerate(UNITS)]
+        with ThreadPoolExecutor(max_workers=max(1, min(len(cmds), os.cpu_count() or 1, 16))) as pool:
+            for res in pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds):
+                if res.returncode != 0:
+                    raise RuntimeError(res.stderr)
+        out_path.write_text("".join(Path(c[-1]).read_text() for c in cmds))
     return out_path
 
 

@@ -1,0 +1,513 @@
+// sc_kernels.h -- the MLP kernel templates of libsigcomp_hip (explicit
+// context windows, teacher-forced compress, persistent decompress) and the
+// host launchers that instantiate them.  Each launcher is defined in a
+// translation unit of its own (sc_ctx.hip, sc_comp.hip, sc_dec.hip), so the
+// large kernels compile in parallel; sc_kernels.hip holds the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/sigcomp_hip.h"
+#include "sc_device.h"
+#include "sc_pipe.h"
+
+namespace sc {
+
+constexpr int RT_TILE = 4;          // rows per MLP tile = 32 * RT_TILE = 128
+constexpr int R_TILE = 32 * RT_TILE;
+constexpr int DEC_RT_MAX = 5;       // decode: up to 160 chunks per workgroup (LDS)
+
+enum CtxOut { OUT_LOGITS = 0, OUT_CDF32 = 1 };
+
+// Coder state of one row between the step segments of a decode: the state
+// of its current chunk, which of its chunks that is and the step it started.
+struct DecState {
+    uint64_t lower, range, point;
+    int32_t rpos, stat, cur, start;
+};
+
+// Host launchers (stream-ordered, no error check: the caller checks
+// hipGetLastError).  The MLP core follows M.pipe.
+template <int MODE>
+void launch_mlp_context(const ModelDev &M, unsigned grid, hipStream_t s, const int64_t *ctx, int64_t rows,
+                        int8_t *logits, int32_t *cdf, int32_t *status);
+void launch_compress_mlp(const ModelDev &M, unsigned grid, hipStream_t s, const uint8_t *tokens, int64_t n_chunks,
+                         const int32_t *tile_start, const int4 *desc, int64_t max_desc, uint2 *pairs);
+template <int RT>
+void launch_decompress(const ModelDev &M, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
+                       const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
+                       int32_t *st, DecState *state, int32_t t_begin, int32_t t_end, int64_t n_second);
+
+namespace {
+
+// Rows of a tile are post-processed four at a time per wavefront: row
+// 4*gi + lane/16 is handled by the 16-lane row lane/16 (see Freq16).
+
+// ---- explicit context windows (GPUBitExactMLPDecoder._ar_step) ----------
+
+
+// MLP core of one tile: the pipelined core when the model allows it.
+template <int CORE, int RT, class AposFn>
+__device__ __forceinline__ void mlp_tile(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act, uint32_t *s_par,
+                                         AposFn apos, int wave, int lane) {
+    if constexpr (CORE != CORE_PLAIN) mlp_rows_pipe<RT, CORE == CORE_PIPE_UNI>(M, s_emb, s_act, s_par, apos, wave, lane);
+    else mlp_rows<RT, (RT <= 4 ? 1 : 2)>(M, s_emb, s_act, s_par, apos, wave, lane);
+}
+// once per kernel, before the first mlp_tile (and a barrier)
+template <int CORE>
+__device__ __forceinline__ void mlp_tile_init(const ModelDev &M, uint32_t *s_par, int wave, int lane) {
+    if constexpr (CORE != CORE_PLAIN) pipe_params_init<CORE == CORE_PIPE_UNI>(M, s_par, wave, lane);
+}
+template <int CORE>
+constexpr int par_lds_dwords() {
+    return CORE == CORE_PLAIN ? PAR_LDS_DWORDS : pipe_par_dwords<CORE == CORE_PIPE_UNI>();
+}
+// activation row layout of the core: padded rows (pipelined) or swizzled rows
+template <bool PIPE>
+constexpr int act_row_bytes() { return PIPE ? PACT_ROW : ACT_ROW; }
+template <bool PIPE>
+__device__ __forceinline__ int act_at(int r, int chunk) { return PIPE ? pact_off(r, chunk) : act_off(r, chunk); }
+
+template <int MODE, int CORE>
+__global__ __launch_bounds__(THREADS, 1) void k_mlp_context(ModelDev M, const int64_t *__restrict__ ctx,
+                                                            int64_t rows, int8_t *__restrict__ logits,
+                                                            int32_t *__restrict__ cdf,
+                                                            int32_t *__restrict__ status) {
+    constexpr bool PIPE = CORE != CORE_PLAIN;
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
+    // rows padded to CTX_STRIDE halfwords: layer 0 reads one position of 32
+    // consecutive rows at a time, which a 128-byte row stride would put in
+    // one LDS bank
+    constexpr int CTX_STRIDE = WIN + 2;
+    __shared__ __attribute__((aligned(16))) uint16_t s_ctx[R_TILE * CTX_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
+    __shared__ double s_lut[VOCAB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
+    const int64_t n_tiles = (rows + R_TILE - 1) / R_TILE;
+    // A tile's 128 x 64 context tokens: 32 per thread, all loads issued
+    // before the first is used (a load / wait / store loop costs one memory
+    // round trip per token).  Element j * THREADS + thread is row 4j + wave,
+    // position lane: each load instruction reads 2 KB.  Addresses and row
+    // limits are formed from per-tile values, so that none is hoisted out of
+    // the tile loop (32 such registers held across the MLP make it spill).
+    constexpr int CTX_PER = R_TILE * WIN / THREADS;
+    static_assert(THREADS == 4 * WIN, "four context rows per load instruction");
+    for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int64_t row0 = tile * R_TILE;
+        const int64_t *src = ctx + row0 * WIN + threadIdx.x;
+        const int64_t lim = rows - row0 - wave;   // element j is in range iff 4j < lim
+        int64_t v[CTX_PER];
+#pragma unroll
+        for (int j = 0; j < CTX_PER; ++j) v[j] = 4 * j < lim ? src[j * THREADS] : 0;
+        __syncthreads();
+        int bad = 0;
+#pragma unroll
+        for (int j = 0; j < CTX_PER; ++j) {
+            const bool ok = (uint64_t)v[j] <= (uint64_t)SOS;
+            bad |= !ok;
+            // element j * THREADS + thread: row 4j + wave, position lane
+            s_ctx[(4 * j + wave) * CTX_STRIDE + lane] = (uint16_t)emb_off(ok ? (int)v[j] : 0, 0);   // table addresses
+        }
+        if (bad) status[0] = SC_STATUS_BAD_TOKEN;
+        __syncthreads();
+        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_ctx[r * CTX_STRIDE + p]; },
+                                wave, lane);
+        if (MODE == OUT_LOGITS) {
+            // 128 rows x 256 bytes, 16-byte chunks, coalesced
+            for (int i = threadIdx.x; i < R_TILE * 16; i += THREADS) {
+                const int r = i >> 4, c = i & 15;
+                if (row0 + r < rows)
+                    *(v4i *)(logits + (row0 + r) * VOCAB + c * 16) = *(const v4i *)(s_act + act_at<PIPE>(r, c));
+            }
+        } else {
+            // two row groups (gi, gi + WAVES) per iteration, see row_frequencies16n
+            for (int gi = wave; gi < R_TILE / 4; gi += 2 * WAVES) {
+                const int rr[2] = {gi * 4 + q4, (gi + WAVES) * 4 + q4};
+                const v4i raw[2] = {*(const v4i *)(s_act + act_at<PIPE>(rr[0], u)),
+                                    *(const v4i *)(s_act + act_at<PIPE>(rr[1], u))};
+                Freq16 fr[2];
+                row_frequencies16n<2>(raw, s_lut, u, fr);
+#pragma unroll
+                for (int n = 0; n < 2; ++n) {
+                    if (row0 + rr[n] < rows) {
+                        int32_t *dst = cdf + (row0 + rr[n]) * (VOCAB + 1) + 16 * u;
+                        uint32_t c = fr[n].ex;
+#pragma unroll
+                        for (int k = 0; k < 16; ++k) {
+                            dst[k] = (int32_t)c;
+                            c += fr[n].f[k];
+                        }
+                        if (u == 15) dst[16] = (int32_t)TOTAL;
+                    }
+                }
+            }
+        }
+    }
+}
+
+
+// ---- compress: teacher-forced MLP fused with the frequency step ----------
+
+// Workgroup b runs tiles b, b + G, b + 2G, ... (G = grid size) of the global
+// tile order.  Every tile costs the same, so the workgroups stay in step and
+// stream the same layer's weights at the same time: each XCD's L2 then
+// serves one weight fragment to all of its CUs (a work counter lets
+// workgroups drift apart, and the L2 cycles through the whole model).  A
+// tile's 128 + 64 tokens (64 of left context) are staged in LDS from its
+// descriptor (k_tile_table), which is loaded while the previous tile's
+// frequency step runs, so a tile waits for one memory round trip.  Output per
+// token: (exclusive cumulative frequency, frequency) of the coded token.
+template <int CORE>
+__global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const uint8_t *__restrict__ tokens,
+                                                             int64_t n_chunks, const int32_t *__restrict__ tile_start,
+                                                             const int4 *__restrict__ desc, int64_t max_desc,
+                                                             uint2 *__restrict__ pairs) {
+    constexpr bool PIPE = CORE != CORE_PLAIN;
+    constexpr int EPI_N = 2;   // row groups per epilogue iteration; R_TILE / 4 is a multiple of EPI_N * WAVES
+    static_assert((R_TILE / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must stay inside the tile");
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R_TILE * act_row_bytes<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
+    __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
+    __shared__ uint16_t s_tok[R_TILE + WIN];
+    __shared__ uint16_t s_apos[R_TILE + WIN];   // emb_off(s_tok[i], 0)
+    __shared__ double s_lut[VOCAB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
+    static_assert(R_TILE + WIN <= THREADS, "one staged token per thread");
+    const int32_t n_tiles = (int32_t)min<int64_t>(tile_start[n_chunks], max_desc);
+    // The next tile's descriptor is loaded during this tile's epilogue.
+    int4 d = (int32_t)blockIdx.x < n_tiles ? desc[blockIdx.x] : make_int4(0, 0, 0, 0);
+    for (int32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int64_t base = (int64_t)(uint32_t)d.x | ((int64_t)d.y << 32);   // token t0 of the chunk
+        const int32_t rem = d.z, t0 = d.w;                                     // L - t0, t0
+        // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
+        const int32_t p = (int32_t)threadIdx.x - WIN;
+        int v = 0;
+        if (threadIdx.x < R_TILE + WIN) v = t0 + p < 0 ? SOS : (p < rem ? (int)tokens[base + p] : 0);
+        __syncthreads();
+        if (threadIdx.x < R_TILE + WIN) {
+            s_tok[threadIdx.x] = (uint16_t)v;
+            s_apos[threadIdx.x] = (uint16_t)emb_off(v, 0);
+        }
+        __syncthreads();
+        mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
+                                wave, lane);
+        if (tile + (int32_t)gridDim.x < n_tiles) d = desc[tile + gridDim.x];
+        uint2 *out = pairs + base;
+        const int32_t valid = min(R_TILE, rem);
+        // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.  The
+        // lane holding the row's token publishes its 16 symbols in the row's
+        // slot; the lane whose index is the token's low 4 bits stores its
+        // (cumulative frequency, frequency) pair.
+        uint32_t *slots = s_slot + wave * (EPI_N * 4 * SLOT_DWORDS);
+        for (int gi = wave; gi * 4 < valid; gi += EPI_N * WAVES) {
+            int rr[EPI_N], sym[EPI_N];
+            v4i raw[EPI_N];
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                rr[n] = (gi + n * WAVES) * 4 + q4;
+                sym[n] = s_tok[rr[n] + WIN];
+                raw[n] = *(const v4i *)(s_act + act_at<PIPE>(rr[n], u));
+            }
+            RowFreq fr[EPI_N];
+            row_freq<EPI_N>(raw, s_lut, u, fr);
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n)
+                if ((sym[n] >> 4) == u) slot_put(slots + (n * 4 + q4) * SLOT_DWORDS, fr[n], u);
+            slot_sync();
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                uint32_t cum, freq;
+                slot_get(slots + (n * 4 + q4) * SLOT_DWORDS, u, cum, freq);
+                if (rr[n] < valid && (sym[n] & 15) == u) out[rr[n]] = make_uint2(cum, freq);
+            }
+        }
+    }
+}
+
+// ---- decompress: persistent autoregressive loop per chunk tile ----------
+
+// Workgroup b owns chunks [b*R, b*R + R).  Each step: MLP on the R context
+// windows (kept as 64-token rings in LDS), the fused frequency step and one
+// decoder step per chunk; the decoded token is appended to the ring.  Chunks
+// are independent, so workgroups never synchronise with each other.
+
+// CpuRangeDecoder.__init__ (cpu_entropy_coding.py:466-474): the point is the
+// first two words, big-endian combined (one word -> w0 << 32)
+__device__ __forceinline__ uint64_t dec_init_point(const uint32_t *w, int cnt, int &take) {
+    uint64_t point = 0;
+    take = cnt < 2 ? cnt : 2;
+    for (int i = 0; i < take; ++i) point = (point << 32) | w[i];
+    if (cnt == 1) point <<= 32;
+    return point;
+}
+
+template <int RT, int CORE>
+__global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
+                                                           const int64_t *__restrict__ word_off,
+                                                           const int32_t *__restrict__ word_cnt,
+                                                           const int32_t *__restrict__ lengths,
+                                                           int64_t n_chunks, uint8_t *__restrict__ tokens,
+                                                           const int64_t *__restrict__ tok_off,
+                                                           int32_t *__restrict__ status,
+                                                           DecState *__restrict__ state, int32_t t_begin,
+                                                           int32_t t_end, int64_t n_second) {
+    // Rows n_chunks - n_second .. n_chunks - 1 each decode a second chunk
+    // after their first one ends: row c continues with chunk
+    // 2 * n_chunks - 1 - c (the n_second chunks after the launch's own, in
+    // reverse order, so that with chunks sorted longest first the longest
+    // second chunk follows the shortest first chunk).
+    constexpr bool PIPE = CORE != CORE_PLAIN;
+    constexpr int R = 32 * RT;
+    constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
+    static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
+    __shared__ __attribute__((aligned(16))) uint8_t s_emb[EMB_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_act[R * act_row_bytes<PIPE>()];
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[R * WIN];
+    // the pipelined core also keeps the ring as embedding-table addresses
+    // (emb_off(token, 0)), written with the token; the plain core converts.
+    // Position-major (apos_at): layer 0 reads one position of 32 consecutive
+    // rows at a time, 32 consecutive halfwords instead of 32 reads 128 bytes
+    // apart in one LDS bank.
+    __shared__ __attribute__((aligned(16))) uint16_t s_apos[PIPE ? R * WIN : 1];
+    auto apos_at = [](int r, int32_t pos) { return (pos & (WIN - 1)) * R + r; };
+    __shared__ __attribute__((aligned(16))) uint32_t s_slot[WAVES * EPI_N * 4 * SLOT_DWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t s_par[par_lds_dwords<CORE>()];
+    __shared__ double s_lut[VOCAB];
+    __shared__ uint64_t s_lower[R], s_range[R], s_point[R];
+    __shared__ int64_t s_woff[R], s_toff[R];
+    __shared__ int32_t s_rpos[R], s_wcnt[R], s_len[R], s_stat[R];
+    // which chunk of the row is current (bit 0: the second one; bit 1: the
+    // row has a second chunk) and the step at which it started
+    __shared__ int32_t s_cur[R], s_start[R];
+    __shared__ int32_t s_maxlen;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, u = lane & 15;
+    const int64_t c0 = (int64_t)blockIdx.x * R;
+    if (threadIdx.x == 0) s_maxlen = 0;
+    __syncthreads();
+    // The workgroup's step count first, from the lengths alone: a later
+    // segment past it returns before reading any coder state, because the
+    // segment that finished these rows saved none (the state buffer then
+    // holds another call's rows, or nothing).
+    for (int r = threadIdx.x; r < R; r += THREADS) {
+        const int64_t c = c0 + r;
+        const bool in = c < n_chunks;
+        // (the plain core's token ring cannot hold the start-of-sequence token)
+        const bool paired = PIPE && in && c >= n_chunks - n_second;
+        const int32_t len1 = in ? lengths[c] : 0;
+        const int32_t len2 = paired ? lengths[2 * n_chunks - 1 - c] : 0;
+        atomicMax(&s_maxlen, max(len1, 0) + max(len2, 0));
+    }
+    __syncthreads();
+    const int32_t maxlen = s_maxlen;
+    const int32_t t_stop = min(maxlen, t_end);
+    // a later segment past this workgroup's longest row: an earlier one
+    // finished its chunks and wrote their status
+    if (t_begin > 0 && t_begin >= t_stop) return;
+    // Here t_begin < t_stop <= maxlen, so the previous segment (if any) ran
+    // this workgroup with t_stop < maxlen and saved every row's state.
+    for (int r = threadIdx.x; r < R; r += THREADS) {
+        const int64_t c = c0 + r;
+        const bool in = c < n_chunks;
+        const bool paired = PIPE && in && c >= n_chunks - n_second;
+        const int32_t len1 = in ? lengths[c] : 0;
+        int32_t cur = 0, start = 0;
+        if (t_begin > 0 && in) {
+            cur = state[c].cur;
+            start = state[c].start;
+        } else if (paired && len1 <= 0) {
+            status[c] = 0;   // an empty first chunk: the second one starts at once
+            cur = 1;
+        }
+        const int64_t cc = cur ? 2 * n_chunks - 1 - c : c;
+        int32_t len = 0, cnt = 0;
+        int64_t woff = 0, toff = 0;
+        if (in) {
+            len = lengths[cc];
+            cnt = word_cnt[cc];
+            woff = word_off[cc];
+            toff = tok_off[cc];
+        }
+        if (t_begin == 0 || !in) {
+            int take;
+            s_point[r] = dec_init_point(words + woff, cnt, take);
+            s_lower[r] = 0ull;
+            s_range[r] = ~0ull;
+            s_rpos[r] = take;
+            s_stat[r] = 0;
+        } else {
+            // a later segment: the state the previous one left
+            const DecState d = state[c];
+            s_lower[r] = d.lower;
+            s_range[r] = d.range;
+            s_point[r] = d.point;
+            s_rpos[r] = d.rpos;
+            s_stat[r] = d.stat;
+        }
+        s_wcnt[r] = cnt;
+        s_woff[r] = woff;
+        s_toff[r] = toff;
+        s_len[r] = len;
+        s_cur[r] = cur | (paired ? 2 : 0);   // bit 1: the row has a second chunk
+        s_start[r] = start;
+    }
+    load_emb_lds(M.emb, s_emb);
+    load_lut_lds(M.lut, s_lut);
+    mlp_tile_init<CORE>(M, s_par, wave, lane);
+    __syncthreads();
+    if (t_begin > 0) {
+        // the context ring: the 64 tokens before t_begin, already written to
+        // `tokens` by the previous segment (segments end on multiples of 64,
+        // where the ring is flushed)
+        for (int i = threadIdx.x; i < R * WIN; i += THREADS) {
+            const int r = i / WIN;
+            const int32_t tp = t_begin - WIN + (i % WIN), rs = tp - s_start[r];
+            if (tp >= 0 && rs < s_len[r]) {
+                // steps before the current chunk started are its start-of-sequence context
+                const int v = rs >= 0 ? (int)tokens[s_toff[r] + rs] : SOS;
+                s_ring[r * WIN + (tp & (WIN - 1))] = (uint8_t)v;
+                if constexpr (PIPE) s_apos[apos_at(r, tp)] = (uint16_t)emb_off(v, 0);
+            }
+        }
+        __syncthreads();
+    }
+    for (int32_t t = t_begin; t < t_stop; ++t) {
+        mlp_tile<CORE, RT>(M, s_emb, s_act, s_par,
+                           [&](int r, int p) {
+                               if (t + p < WIN) return emb_off(SOS, 0);
+                               if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
+                               else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
+                           },
+                           wave, lane);
+        // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
+        // _decode_partition (cpu_entropy_coding.py:230-266): every lane of a
+        // row computes the row's quantile; the lane whose 16 symbols hold it
+        // publishes them in the row's slot and the lane that finds the
+        // symbol there (its interval holds the quantile) stores the new
+        // state.  The word a renormalisation would shift in is loaded before
+        // the frequency work (whether or not this step needs it) so its
+        // latency is hidden.
+        uint32_t *slots = s_slot + wave * (EPI_N * 4 * SLOT_DWORDS);
+        for (int gi = wave; gi < R / 4; gi += EPI_N * WAVES) {
+            int rr[EPI_N];
+            uint64_t lower[EPI_N], range[EPI_N], point[EPI_N];
+            int32_t rpos[EPI_N];
+            uint32_t wnext[EPI_N];
+            bool active[EPI_N], last1[EPI_N];
+            v4i raw[EPI_N];
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                const int r = (gi + n * WAVES) * 4 + q4;
+                rr[n] = r;
+                const int32_t rs = t - s_start[r], len = s_len[r];
+                active[n] = rs < len && s_stat[r] == 0;
+                last1[n] = s_cur[r] == 2 && rs == len - 1;   // the row's first chunk ends with this step
+                lower[n] = s_lower[r];
+                range[n] = s_range[r];
+                point[n] = s_point[r];
+                rpos[n] = s_rpos[r];
+                wnext[n] = rpos[n] < s_wcnt[r] ? words[s_woff[r] + rpos[n]] : 0u;
+                raw[n] = *(const v4i *)(s_act + act_at<PIPE>(r, u));
+            }
+            RowFreq fr[EPI_N];
+            row_freq<EPI_N>(raw, s_lut, u, fr);
+            uint32_t q[EPI_N];
+            bool ok[EPI_N];
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                const uint64_t scale = range[n] >> 24;
+                q[n] = 0;
+                ok[n] = scale != 0 && dec_quantile(point[n] - lower[n], scale, q[n]);
+                if (ok[n] && q[n] - fr[n].ex < fr[n].tot) slot_put(slots + (n * 4 + q4) * SLOT_DWORDS, fr[n], u);
+            }
+            slot_sync();
+#pragma unroll
+            for (int n = 0; n < EPI_N; ++n) {
+                const int r = rr[n];
+                uint32_t cum, freq;
+                const uint32_t owner = slot_get(slots + (n * 4 + q4) * SLOT_DWORDS, u, cum, freq);
+                if (active[n] && ok[n] && q[n] - cum < freq) {
+                    const uint64_t scale = range[n] >> 24;
+                    uint64_t lo = lower[n] + mul_scale(scale, cum), ra = mul_scale(scale, freq), pt = point[n];
+                    int32_t rp = rpos[n];
+                    if (ra < (1ull << 32)) {
+                        lo <<= 32;
+                        ra <<= 32;
+                        pt = (pt << 32) | wnext[n];
+                        rp += 1;
+                    }
+                    s_lower[r] = lo;
+                    s_range[r] = ra;
+                    s_point[r] = pt;
+                    s_rpos[r] = rp;
+                    s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)(owner * 16 + u);
+                    if constexpr (PIPE) s_apos[apos_at(r, t)] = (uint16_t)emb_off(owner * 16 + u, 0);
+                }
+                if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
+                if (last1[n]) {
+                    // write out the first chunk's last tokens, then start the
+                    // second chunk from the next step with a start-of-sequence
+                    // context
+                    slot_sync();
+                    const int64_t c = c0 + r;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - s_start[r];
+                        if (pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
+                        if constexpr (PIPE) s_apos[apos_at(r, 4 * u + k)] = (uint16_t)emb_off(SOS, 0);
+                    }
+                    if (u == 0) {
+                        status[c] = s_stat[r];
+                        const int64_t c2 = 2 * n_chunks - 1 - c;
+                        const int32_t cnt = word_cnt[c2];
+                        const int64_t woff = word_off[c2];
+                        int take;
+                        s_point[r] = dec_init_point(words + woff, cnt, take);
+                        s_lower[r] = 0ull;
+                        s_range[r] = ~0ull;
+                        s_rpos[r] = take;
+                        s_stat[r] = 0;
+                        s_wcnt[r] = cnt;
+                        s_woff[r] = woff;
+                        s_toff[r] = tok_off[c2];
+                        s_len[r] = lengths[c2];
+                        s_cur[r] = 3;
+                        s_start[r] = t + 1;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // every 64 steps (and at the end) the ring holds the last 64 tokens
+        // of each chunk: one wavefront per chunk writes them as one 64-byte
+        // run instead of a byte per step
+        if ((t & (WIN - 1)) == WIN - 1 || t == maxlen - 1) {
+            const int32_t p = (t & ~(WIN - 1)) + lane;
+            for (int r = wave; r < R; r += WAVES) {
+                const int32_t rs = p - s_start[r];
+                if (p <= t && rs >= 0 && rs < s_len[r]) tokens[s_toff[r] + rs] = s_ring[r * WIN + lane];
+            }
+        }
+    }
+    for (int r = threadIdx.x; r < R; r += THREADS)
+        if (c0 + r < n_chunks) {
+            const int64_t c = c0 + r;
+            const int cur = s_cur[r] & 1;
+            status[cur ? 2 * n_chunks - 1 - c : c] = s_stat[r];
+            if (t_stop < maxlen)
+                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], s_stat[r], cur, s_start[r]};
+        }
+}
+
+}  // namespace
+}  // namespace sc

@@ -520,10 +520,13 @@ def test_decompress_one_million_chunks(codecs, capfd, monkeypatch):
     assert np.array_equal(back, tokens)
 
 
-def _decode_direct(codec, words, woff, wcnt, lengths):
+def _decode_direct(codec, words, woff, wcnt, lengths, host_lengths=True, ws_fill=None):
     """sc_decompress_chunks on the chunks in the order given (the C ABI does
     not sort) -> (tokens of all chunks in chunk order, per-chunk status).
-    Status starts at -1 so that a chunk whose status is never written shows."""
+    Status starts at -1 so that a chunk whose status is never written shows.
+    host_lengths: pass the host copy of the lengths (plan on the host) or
+    NULL (plan statistics on the device); ws_fill: byte written over the
+    workspace first (state left by an unrelated call)."""
     from sigcomp_amd import _hip
     n = len(lengths)
     tok_off = np.zeros(n, np.int64)
@@ -534,9 +537,14 @@ def _decode_direct(codec, words, woff, wcnt, lengths):
     t_len, t_toff = d(lengths.astype(np.int32)), d(tok_off)
     tokens = torch.zeros(max(n_tok, 1), dtype=torch.uint8, device="cuda")
     status = torch.full((n,), -1, dtype=torch.int32, device="cuda")
+    ws = codec._decompress_workspace(n)
+    if ws_fill is not None:
+        ws.fill_(ws_fill)
+    len_host = np.ascontiguousarray(lengths, np.int32)   # referenced until the call returns
     _hip.check(_hip.lib().sc_decompress_chunks(
         codec.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt), _hip.ptr(t_len), n,
-        _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status), _hip.stream_ptr()))
+        _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status),
+        len_host.ctypes.data if host_lengths else None, _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
     torch.cuda.synchronize()
     return tokens.cpu().numpy()[:n_tok], status.cpu().numpy(), tok_off
 
@@ -639,8 +647,10 @@ def test_decompress_status_survives_later_segments(codecs, monkeypatch):
     woff, wcnt = woff.copy(), wcnt.copy()
     woff[40], wcnt[40] = len(words) - 2, 2
     monkeypatch.setenv("SC_HIP_DEC_SEG", "64")
-    for _ in range(2):   # the second call starts from the first call's decode state buffer
-        back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths)
+    # a workspace holding another call's state (every row's "current chunk"
+    # field nonzero): launches past a workgroup's rows must not read it
+    for host_lengths, fill in ((True, None), (False, 1), (True, 255)):
+        back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths, host_lengths, fill)
         expect = np.zeros(64, np.int32)
         expect[40] = 2
         assert np.array_equal(status, expect)
