@@ -1,145 +1,118 @@
-"""Per-read chunking and ``<H``-length framing of range-coded chunks.
+"""Per-read chunking and SIG2 chunk framing around the GPU codec.
 
-Restates ``ReadFramingMixin.batch_inference_reads``
-(``cpu_compression.py:28-84``), which the reference GPU codec inherits
-through its MRO (``main.py:215``): each read's tokens are cut into
-``chunk_len`` chunks; a read's payload is the concatenation, per chunk, of
-a little-endian uint16 byte length and the chunk's little-endian u32 words.
-An empty read has an empty payload.  Decoding validates nonzero sizes that
-are multiples of four, no truncation and no trailing bytes.
+``ReadFramingMixin.batch_inference_reads`` has the contract of the
+reference's mixin (``cpu_compression.py:28-84``, inherited by the reference
+GPU codec through ``main.py:215``): a read's tokens are cut into
+``chunk_len``-token chunks, every chunk is range coded independently, and a
+read's payload is, per chunk, a little-endian uint16 byte count followed by
+the chunk's little-endian u32 words (an empty read has an empty payload).
+Decoding checks every frame and the read's token count.
+
+All reads of a call are handled together: the chunk layout is computed with
+numpy, framing and parsing run in the multithreaded host library
+(``sigcomp_amd._host``: ``sc_host_frame`` / ``sc_host_parse``), and the codec
+sees every chunk of the call at once (``compress_flat`` / ``decompress_flat``
+when it has them, else ``compress_chunks`` / ``decompress_chunks``).
 """
 
 from __future__ import annotations
 
-import struct
-
 import numpy as np
 
-_CHUNK_LENGTH = struct.Struct("<H")
+from . import _host
 
 
-def as_symbols(values) -> np.ndarray:
-    """``cpu_compression.py:18-25``: one-dimensional integer tokens in [0, 255]."""
-    values = np.asarray(values)
-    if values.ndim != 1:
-        raise ValueError("Each token sequence must be one-dimensional")
-    if values.size and (values.dtype.kind not in "iu" or np.any(values < 0) or np.any(values > 255)):
-        raise ValueError("Signal tokens must be integers in [0, 255]")
-    return np.ascontiguousarray(values, dtype=np.uint8)
+def token_array(values) -> np.ndarray:
+    """One read's or chunk's tokens as a contiguous uint8 array; raises
+    ValueError unless they are a 1-D integer sequence in [0, 255]."""
+    a = np.asarray(values)
+    if a.ndim != 1:
+        raise ValueError(f"token sequences are one-dimensional, got shape {a.shape}")
+    if a.size:
+        if a.dtype.kind not in "iu":
+            raise ValueError(f"tokens must be integers, got dtype {a.dtype}")
+        if a.dtype != np.uint8 and (int(a.min()) < 0 or int(a.max()) > 255):
+            raise ValueError("tokens must lie in [0, 255]")
+    return np.ascontiguousarray(a, dtype=np.uint8)
 
 
-def split_into_chunks(tokens, chunk_len: int) -> list:
-    tokens = as_symbols(tokens)
-    return [tokens[i:i + chunk_len] for i in range(0, len(tokens), chunk_len)]
+def chunk_layout(read_lengths: np.ndarray, chunk_len: int):
+    """Chunks of every read in read order -> (first chunk of each read
+    [n_reads + 1], token count of each chunk [n_chunks] int32)."""
+    read_lengths = np.asarray(read_lengths, np.int64)
+    per_read = -(-read_lengths // chunk_len)
+    first = np.zeros(len(read_lengths) + 1, np.int64)
+    np.cumsum(per_read, out=first[1:])
+    sizes = np.full(int(first[-1]), chunk_len, np.int32)
+    nonempty = per_read > 0
+    # a read's last chunk holds what the full ones leave
+    sizes[first[1:][nonempty] - 1] = (read_lengths[nonempty] - (per_read[nonempty] - 1) * chunk_len)
+    return first, sizes
 
 
-def frame_chunks(encoded_chunks) -> bytes:
-    framed = bytearray()
-    for chunk in encoded_chunks:
-        if len(chunk) > 65535:
-            raise ValueError("Compressed chunk exceeds the SIG2 uint16 frame; "
-                             "compress with a smaller --chunk-len")
-        framed.extend(_CHUNK_LENGTH.pack(len(chunk)))
-        framed.extend(chunk)
-    return bytes(framed)
-
-
-def parse_framed(data: bytes, length: int, chunk_len: int):
-    """-> (list of chunk byte strings, list of chunk token counts)."""
-    if int(length) != length or length < 0:
-        raise ValueError("Token lengths must be nonnegative integers")
-    chunks, lengths = [], []
-    remaining, pos = int(length), 0
-    while remaining:
-        if pos + _CHUNK_LENGTH.size > len(data):
-            raise ValueError("Truncated SIG2 chunk length")
-        size, = _CHUNK_LENGTH.unpack_from(data, pos)
-        pos += _CHUNK_LENGTH.size
-        if size == 0 or size % 4 or pos + size > len(data):
-            raise ValueError("Invalid or truncated SIG2 range-coded chunk")
-        count = min(chunk_len, remaining)
-        chunks.append(data[pos:pos + size])
-        lengths.append(count)
-        pos += size
-        remaining -= count
-    if pos != len(data):
-        raise ValueError("Trailing SIG2 chunk data disagrees with token length")
-    return chunks, lengths
+def _words_of(encoded) -> tuple:
+    """Encoded chunk byte strings -> (u32 words, offsets, counts)."""
+    cnt = np.fromiter((len(e) // 4 for e in encoded), np.int32, count=len(encoded))
+    off = np.zeros(len(encoded), np.int64)
+    np.cumsum(cnt[:-1], out=off[1:])
+    words = np.frombuffer(b"".join(encoded), "<u4").astype(np.uint32) if cnt.sum() else np.zeros(0, np.uint32)
+    return words, off, cnt
 
 
 class ReadFramingMixin:
     """Drop-in for the reference mixin: ``batch_inference_reads`` on top of
-    ``self.compress_chunks`` / ``self.decompress_chunks`` and ``self.chunk_len``.
-
-    Codecs that also provide ``compress_flat`` / ``decompress_flat`` (the GPU
-    codec does) take the batched path: chunking, framing and parsing of all
-    reads in one call each to the host library (``sigcomp_amd._host``), with
-    the same bytes and the same errors."""
+    the codec's chunk calls and ``self.chunk_len``."""
 
     def batch_inference_reads(self, list_of_reads=None, list_of_compressed_reads=None,
                               list_of_lengths=None, batch_size=64, use_tqdm=False, prob_quant=0):
         if batch_size < 1:
             raise ValueError("batch_size must be positive")
-        flat = hasattr(self, "compress_flat") and hasattr(self, "decompress_flat")
-        chunks, lengths, mapping = [], [], []
         if list_of_reads is not None:
-            if flat:
-                return self._compress_reads_flat(list_of_reads, batch_size)
-            for read in list_of_reads:
-                begin = len(chunks)
-                chunks.extend(split_into_chunks(read, self.chunk_len))
-                mapping.append((begin, len(chunks)))
-            encoded = self.compress_chunks(chunks, max_batch_size=batch_size, use_tqdm=use_tqdm)
-            return [frame_chunks(encoded[b:e]) for b, e in mapping]
-
+            return self._compress_reads(list_of_reads, batch_size, use_tqdm)
         if list_of_compressed_reads is None or list_of_lengths is None:
             raise ValueError("Compressed reads and token lengths are required")
         if len(list_of_compressed_reads) != len(list_of_lengths):
             raise ValueError("Compressed read and token length counts differ")
-        if flat:
-            return self._decompress_reads_flat(list_of_compressed_reads, list_of_lengths)
-        for data, length in zip(list_of_compressed_reads, list_of_lengths):
-            begin = len(chunks)
-            parts, counts = parse_framed(data, length, self.chunk_len)
-            chunks.extend(parts)
-            lengths.extend(counts)
-            mapping.append((begin, len(chunks)))
-        decoded = self.decompress_chunks(chunks, lengths, max_batch_size=batch_size,
-                                         use_tqdm=use_tqdm)
-        return [np.concatenate(decoded[b:e]) if e > b else np.empty(0, dtype=np.uint8)
-                for b, e in mapping]
+        return self._decompress_reads(list_of_compressed_reads, list_of_lengths, batch_size, use_tqdm)
 
-    def _compress_reads_flat(self, list_of_reads, batch_size):
-        from . import _host
-        reads = [as_symbols(r) for r in list_of_reads]
+    def _compress_reads(self, list_of_reads, batch_size, use_tqdm):
+        reads = [token_array(r) for r in list_of_reads]
         cl = int(self.chunk_len)
-        lens = np.fromiter((len(r) for r in reads), np.int64, count=len(reads))
-        nch = (lens + cl - 1) // cl
-        chunk_begin = np.zeros(len(reads) + 1, np.int64)
-        np.cumsum(nch, out=chunk_begin[1:])
-        n_chunks = int(chunk_begin[-1])
-        chunk_len = np.full(n_chunks, cl, np.int32)
-        last = chunk_begin[1:][nch > 0] - 1
-        chunk_len[last] = (lens[nch > 0] - (nch[nch > 0] - 1) * cl).astype(np.int32)
+        first, sizes = chunk_layout([r.size for r in reads], cl)
         tokens = np.concatenate(reads) if reads else np.zeros(0, np.uint8)
-        words, word_off, word_cnt = self.compress_flat(tokens, chunk_len, batch_size)
+        if hasattr(self, "compress_flat"):
+            words, word_off, word_cnt = self.compress_flat(tokens, sizes, batch_size, use_tqdm=use_tqdm)
+        else:
+            starts = np.zeros(len(sizes), np.int64)
+            np.cumsum(sizes[:-1], out=starts[1:])
+            encoded = self.compress_chunks([tokens[s:s + n] for s, n in zip(starts, sizes)],
+                                           max_batch_size=batch_size, use_tqdm=use_tqdm)
+            words, word_off, word_cnt = _words_of(encoded)
         buf, bounds = _host.frame(words, word_off, word_cnt)
-        return [buf[bounds[chunk_begin[r]]:bounds[chunk_begin[r + 1]]].tobytes() for r in range(len(reads))]
+        return [buf[bounds[first[r]]:bounds[first[r + 1]]].tobytes() for r in range(len(reads))]
 
-    def _decompress_reads_flat(self, payloads, list_of_lengths):
-        from . import _host
+    def _decompress_reads(self, payloads, list_of_lengths, batch_size, use_tqdm):
         bad_len = next((i for i, x in enumerate(list_of_lengths) if int(x) != x or x < 0), None)
         if bad_len is not None:
-            # the reference checks reads in order: a framing error of an
-            # earlier read is raised first
+            # reads are checked in order: a framing error of an earlier read
+            # is raised first
             _host.parse(payloads[:bad_len], [int(x) for x in list_of_lengths[:bad_len]], int(self.chunk_len))
             raise ValueError("Token lengths must be nonnegative integers")
-        tokens = np.fromiter((int(x) for x in list_of_lengths), np.int64, count=len(list_of_lengths))
-        pr = _host.parse(payloads, tokens, int(self.chunk_len))
-        tok, tok_off = self.decompress_flat(pr["words"], pr["word_off"], pr["word_cnt"], pr["tok_cnt"])
+        n_tok = np.fromiter((int(x) for x in list_of_lengths), np.int64, count=len(list_of_lengths))
+        pr = _host.parse(payloads, n_tok, int(self.chunk_len))
+        if hasattr(self, "decompress_flat"):
+            tok, tok_off = self.decompress_flat(pr["words"], pr["word_off"], pr["word_cnt"], pr["tok_cnt"],
+                                                use_tqdm=use_tqdm)
+        else:
+            w = pr["words"]
+            encoded = [w[o:o + c].tobytes() for o, c in zip(pr["word_off"], pr["word_cnt"])]
+            dec = self.decompress_chunks(encoded, [int(x) for x in pr["tok_cnt"]], max_batch_size=batch_size,
+                                         use_tqdm=use_tqdm)
+            tok = np.concatenate(dec) if dec else np.zeros(0, np.uint8)
+            tok_off = np.zeros(len(dec), np.int64)
+            np.cumsum(pr["tok_cnt"][:-1], out=tok_off[1:])
         out = []
-        for r, n in enumerate(tokens):
-            c = pr["chunk_begin"][r]
-            start = tok_off[c] if pr["frames"][r] else 0
+        for r, n in enumerate(n_tok):
+            start = tok_off[pr["chunk_begin"][r]] if pr["frames"][r] else 0
             out.append(tok[start:start + n] if n else np.empty(0, dtype=np.uint8))
         return out

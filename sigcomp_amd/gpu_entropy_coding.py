@@ -28,6 +28,24 @@ def build_integer_exp_lut(output_scale, lut_precision_bits=38):
     return torch.from_numpy(_build_lut_np(output_scale, lut_precision_bits))
 
 
+def quantize_probs_to_cdf(probs, precision=PRECISION, deterministic=False):
+    """Float probabilities [..., V] -> int64 CDF [..., V + 1] summing to
+    2**precision (``gpu_entropy_coding.py:54-75``; no caller on the codec
+    path, kept for the module's interface).  Each frequency is
+    floor(p * 2**precision) in the tensor's own float type, at least 1; the
+    surplus or deficit against 2**precision is taken from the first largest
+    frequency (``deterministic`` selects that index explicitly in the
+    reference; torch's argmax already returns the first maximum, so both
+    settings give the same table).  Runs where `probs` lives."""
+    total = 1 << int(precision)
+    freqs = torch.floor(probs * total).to(torch.int64).clamp_min(1)
+    excess = freqs.sum(dim=-1, keepdim=True) - total
+    freqs.scatter_add_(-1, freqs.argmax(dim=-1, keepdim=True), -excess)
+    cdf = torch.zeros(*freqs.shape[:-1], freqs.shape[-1] + 1, dtype=torch.int64, device=freqs.device)
+    torch.cumsum(freqs, dim=-1, out=cdf[..., 1:])
+    return cdf
+
+
 def _device_of(t: torch.Tensor) -> torch.device:
     if not t.is_cuda:
         raise ValueError("GPU entropy coding needs CUDA (HIP) tensors")

@@ -192,7 +192,9 @@ def export_npz(model: IntModel, path) -> None:
     np.savez_compressed(path, **arrays)
 
 
-def _from_npz(path, window_size) -> IntModel:
+def _from_npz(path, dim, num_dec_layers, window_size) -> IntModel:
+    """An integer export; its architecture must be the one asked for, as
+    ``load_cpu_decoder`` requires of a checkpoint (``cpu_int_inference.py:395-445``)."""
     with np.load(path, allow_pickle=False) as z:
         layers = [make_layer(z[f"w{i}"], z[f"b{i}"], z[f"m0_{i}"], z[f"shift{i}"],
                              bool(z[f"relu{i}"])) for i in range(int(z["n_layers"]))]
@@ -200,6 +202,12 @@ def _from_npz(path, window_size) -> IntModel:
                          window=int(z["window"]), output_scale=float(z["output_scale"]),
                          input_scale=float(z["input_scale"]),
                          exp_lut=np.ascontiguousarray(z["exp_lut"]))
+    if model.emb.ndim != 2 or model.emb.shape != (SOS_TOKEN + 1, dim // 2):
+        raise ValueError("Checkpoint embedding shape does not match --dim")
+    if len(model.layers) != num_dec_layers + 1:
+        raise ValueError("Checkpoint layer count does not match --num-dec-layers")
+    if any(layer.n != dim * 2 for layer in model.layers[:-1]):
+        raise ValueError("Checkpoint hidden width does not match --dim")
     if window_size is not None and int(window_size) != model.window:
         raise ValueError("Model window size does not match --window-size")
     return model
@@ -213,7 +221,7 @@ def load_int_model(model_path=None, dim=None, num_dec_layers=None, window_size=N
     if dim < 2 or num_dec_layers < 0 or (window_size is not None and int(window_size) < 1):
         raise ValueError("Invalid MLP architecture")
     if path.suffix == ".npz":
-        model = _from_npz(path, window_size)
+        model = _from_npz(path, dim, num_dec_layers, window_size)
     else:
         model = _from_pth(path, dim, num_dec_layers, 64 if window_size is None else int(window_size))
     validate_model(model)

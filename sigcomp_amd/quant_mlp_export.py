@@ -26,13 +26,24 @@ import numpy as np
 import torch
 
 from . import _hip
-from .framing import ReadFramingMixin, as_symbols
+from .framing import ReadFramingMixin, token_array
 from .model_io import (DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH,  # noqa: F401
                        DEFAULT_QUANT_MODEL_PATH, DEFAULT_LSB_SETTING_FOR_LOSSY_MODEL, IntModel,
                        SOS_TOKEN, VOCAB_SIZE, load_int_model)
 
 # Chunks staged per kernel launch (bounds host/device staging memory only).
 _MIN_LAUNCH_CHUNKS = 1 << 16
+
+
+def _progress(it, use_tqdm, desc):
+    """`it`, wrapped in a tqdm progress bar when asked for (and installed)."""
+    if not use_tqdm:
+        return it
+    try:
+        from tqdm import tqdm
+    except ImportError:
+        return it
+    return tqdm(it, desc=desc)
 
 
 def _to_device(a, dev):
@@ -168,7 +179,7 @@ class QuantMLPCompression(ReadFramingMixin):
     def compress_chunks(self, chunks, max_batch_size=64, use_perfect=False, use_tqdm=False):
         if max_batch_size < 1:
             raise ValueError("max_batch_size must be positive")
-        chunks = [as_symbols(c) for c in chunks]
+        chunks = [token_array(c) for c in chunks]
         if any(len(c) > self.chunk_len for c in chunks):
             raise ValueError("A token chunk exceeds chunk_len")
         n = len(chunks)
@@ -176,15 +187,16 @@ class QuantMLPCompression(ReadFramingMixin):
             return []
         lengths = np.fromiter((len(c) for c in chunks), dtype=np.int32, count=n)
         tokens = np.concatenate(chunks)
-        words, word_off, word_cnt = self.compress_flat(tokens, lengths, max_batch_size)
+        words, word_off, word_cnt = self.compress_flat(tokens, lengths, max_batch_size, use_tqdm=use_tqdm)
         return [words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in range(n)]
 
-    def compress_flat(self, tokens, lengths, max_batch_size=64):
+    def compress_flat(self, tokens, lengths, max_batch_size=64, use_tqdm=False):
         """Compress chunks given as concatenated uint8 tokens and int32 chunk
         lengths -> (uint32 words of all chunks, densely packed, per-chunk
         word offsets, per-chunk word counts).  Each chunk is coded
         independently; launches cover up to max(max_batch_size, 65536)
-        chunks."""
+        chunks (use_tqdm: a progress bar over them, as the reference shows
+        one over its batches)."""
         tokens = np.ascontiguousarray(tokens, np.uint8)
         lengths = np.ascontiguousarray(lengths, np.int32)
         if np.any(lengths < 0) or np.any(lengths > self.chunk_len):
@@ -195,7 +207,7 @@ class QuantMLPCompression(ReadFramingMixin):
             return np.zeros(0, np.uint32), np.zeros(0, np.int64), np.zeros(0, np.int32)
         per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
         parts, tok0 = [], 0
-        for s in range(0, len(lengths), per):
+        for s in _progress(range(0, len(lengths), per), use_tqdm, "Compressing chunks (GPU)"):
             ln = lengths[s:s + per]
             nt = int(ln.sum())
             parts.append(self._compress_batch(tokens[tok0:tok0 + nt], ln))
@@ -254,6 +266,12 @@ class QuantMLPCompression(ReadFramingMixin):
 
     # ---------------------------------------------------------- decompress
 
+    def _decompress_workspace(self, n):
+        """Per-call decode state (sc_decompress_workspace_bytes): a tensor
+        from torch's stream-ordered allocator, so calls never share it."""
+        nbytes = int(_hip.lib().sc_decompress_workspace_bytes(n))
+        return torch.empty(nbytes, dtype=torch.uint8, device=self.hip.device)
+
     def decompress_chunks(self, compressed_bytes_list, valid_lengths, max_batch_size=64,
                           use_perfect=False, use_tqdm=False):
         if max_batch_size < 1:
@@ -267,7 +285,7 @@ class QuantMLPCompression(ReadFramingMixin):
                 raise ValueError("Invalid range-coded chunk for its token length")
         per = max(int(max_batch_size), _MIN_LAUNCH_CHUNKS)
         out = []
-        for s in range(0, len(compressed_bytes_list), per):
+        for s in _progress(range(0, len(compressed_bytes_list), per), use_tqdm, "Decompressing chunks (GPU)"):
             out.extend(self._decompress_batch(compressed_bytes_list[s:s + per],
                                               valid_lengths[s:s + per]))
         return out
@@ -285,7 +303,7 @@ class QuantMLPCompression(ReadFramingMixin):
         tok, tok_off = self.decompress_flat(flat, word_off, cnt, lengths)
         return [tok[tok_off[i]:tok_off[i] + lengths[i]].copy() for i in range(n)]
 
-    def decompress_flat(self, words, word_off, word_cnt, lengths):
+    def decompress_flat(self, words, word_off, word_cnt, lengths, use_tqdm=False):
         """Decompress chunks given as one uint32 word array with per-chunk
         word offsets / counts and token lengths -> (uint8 tokens of all
         chunks concatenated in chunk order, per-chunk token offsets).  One
@@ -320,11 +338,13 @@ class QuantMLPCompression(ReadFramingMixin):
         t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(lengths[order]), d(tok_off[order])
         tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)
         status = torch.empty(n, dtype=torch.int32, device=dev)
+        len_host = np.ascontiguousarray(lengths[order])
         with torch.cuda.device(dev):
+            ws = self._decompress_workspace(n)
             _hip.check(_hip.lib().sc_decompress_chunks(
                 self.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt),
                 _hip.ptr(t_len), n, _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status),
-                _hip.stream_ptr()))
+                len_host.ctypes.data, _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
         st = status.cpu().numpy()
         if st.any():
             raise ValueError("invalid range stream or mismatching entropy model in chunk "

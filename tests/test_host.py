@@ -1,8 +1,8 @@
 """Host library (libsigcomp_host.so): signal split / reassembly and SIG2 chunk
 framing, against the numpy restatement of main.py's transforms
-(oracle/signal_ref.py), closed forms, the reference's framing loop
-(sigcomp_amd.framing.parse_framed / frame_chunks, restating
-cpu_compression.py:28-84) and the reference's golden framed reads."""
+(oracle/signal_ref.py), closed forms, the restated framing loop
+(oracle/framing_ref.py, cpu_compression.py:28-84) and the reference's
+golden framed reads."""
 
 import numpy as np
 import pytest
@@ -115,7 +115,7 @@ def test_reassemble_and_split_errors():
 
 def test_frame_matches_python_framing():
     _host = _lib_or_skip()
-    from sigcomp_amd.framing import frame_chunks
+    from framing_ref import frame as frame_chunks
     rng = np.random.default_rng(3)
     cnt = rng.integers(1, 40, 50).astype(np.int32)
     cap = cnt + rng.integers(0, 3, 50)
@@ -131,7 +131,7 @@ def test_frame_matches_python_framing():
 
 
 def _payload(rng, tokens, chunk_len):
-    from sigcomp_amd.framing import frame_chunks
+    from framing_ref import frame as frame_chunks
     n = (tokens + chunk_len - 1) // chunk_len
     return frame_chunks([rng.integers(0, 2**32, rng.integers(1, 9), dtype=np.uint64).astype(np.uint32).tobytes()
                          for _ in range(n)])
@@ -139,7 +139,7 @@ def _payload(rng, tokens, chunk_len):
 
 def test_parse_matches_python_parse_and_errors():
     _host = _lib_or_skip()
-    from sigcomp_amd.framing import parse_framed
+    from framing_ref import parse as parse_framed
     rng = np.random.default_rng(4)
     tokens = [0, 1, 7, 8, 9, 30, 64]
     payloads = [_payload(rng, t, 8) for t in tokens]
@@ -170,14 +170,14 @@ class _OracleCodec:
     def __init__(self, oracle_mod, om, chunk_len=2048):
         self.o, self.om, self.chunk_len = oracle_mod, om, chunk_len
 
-    def compress_flat(self, tokens, lengths, max_batch_size=64):
+    def compress_flat(self, tokens, lengths, max_batch_size=64, use_tqdm=False):
         off = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
         enc = self.o.compress_chunks(self.om, [tokens[o:o + n] for o, n in zip(off, lengths)])
         cnt = np.array([len(e) // 4 for e in enc], np.int32)
         words = np.frombuffer(b"".join(enc), np.uint32) if enc else np.zeros(0, np.uint32)
         return words, np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(np.int64), cnt
 
-    def decompress_flat(self, words, word_off, word_cnt, lengths):
+    def decompress_flat(self, words, word_off, word_cnt, lengths, use_tqdm=False):
         dec = self.o.decompress_chunks(self.om, [words[o:o + c].tobytes() for o, c in zip(word_off, word_cnt)],
                                        list(lengths))
         tok_off = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)

