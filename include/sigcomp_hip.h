@@ -231,6 +231,22 @@ int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int
                          const int32_t *lengths_host, void *workspace, int64_t workspace_bytes,
                          void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  sc_decompress_chunks with its workspace replaced by a
+ * static device array the library holds on each GPU it runs on until the
+ * process ends (SC_STATIC_DEC_MAX_CHUNKS chunks of coder state, 2.5 MiB);
+ * the call allocates nothing.  n_chunks above SC_STATIC_DEC_MAX_CHUNKS ->
+ * SC_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (on different streams or threads) race.  With
+ * lengths_host NULL the call waits for its stream, as sc_decompress_chunks
+ * does. */
+#define SC_STATIC_DEC_MAX_CHUNKS 65536
+int sc_decompress_chunks_static(const sc_model *model, const uint32_t *words, const int64_t *word_off,
+                                const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,
+                                uint8_t *tokens, const int64_t *tok_off, int32_t *status,
+                                const int32_t *lengths_host, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

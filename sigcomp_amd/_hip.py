@@ -26,8 +26,12 @@ EXPORTED = (
     "sc_model_core",
     "sc_mlp_forward", "sc_mlp_forward_cdf", "sc_logits_to_cdf", "sc_encode_step",
     "sc_encode_seal", "sc_decode_step", "sc_compress_workspace_bytes", "sc_compress_chunks",
-    "sc_decompress_workspace_bytes", "sc_decompress_chunks", "sc_gather_words", "sc_mfma_burn_i8",
+    "sc_decompress_workspace_bytes", "sc_decompress_chunks", "sc_decompress_chunks_static",
+    "sc_gather_words", "sc_mfma_burn_i8",
 )
+
+# chunks per sc_decompress_chunks_static call (SC_STATIC_DEC_MAX_CHUNKS)
+STATIC_DEC_MAX_CHUNKS = 65536
 
 
 class LayerDesc(ctypes.Structure):
@@ -90,6 +94,7 @@ def lib():
         L.sc_decompress_workspace_bytes.argtypes = [_I64]
         L.sc_decompress_workspace_bytes.restype = _I64
         L.sc_decompress_chunks.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P]
+        L.sc_decompress_chunks_static.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P]
         L.sc_gather_words.argtypes = [_P, _P, _P, _I64, _P, _P, _P]
         L.sc_mfma_burn_i8.argtypes = [_P, _I32, _I32, _P, _P]
         for name in EXPORTED:

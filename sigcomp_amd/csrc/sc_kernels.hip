@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -458,6 +459,43 @@ std::vector<int> dec_plan(int64_t units) {
 // all of them (memory-side traffic of a c3 decode: 530 -> 215 GB).
 constexpr int DEC_SEG_STEPS = 256;
 
+// Decode state of sc_decompress_chunks_static: a file-scope device array
+// (each GPU the library runs on holds its own copy until the process ends)
+// with the coder state of up to SC_STATIC_DEC_MAX_CHUNKS chunks, then the
+// launch plan's four length statistics.  Host code never passes `scratch`
+// itself (in host code the name is a stand-in, not a device address): the
+// address of the current device's copy comes from hipGetSymbolAddress.
+constexpr int64_t SCRATCH_STATE_BYTES = ((int64_t)SC_STATIC_DEC_MAX_CHUNKS * sizeof(DecState) + 255) / 256 * 256;
+constexpr int64_t SCRATCH_BYTES = SCRATCH_STATE_BYTES + 256;
+__device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's copy of `scratch` (resolved once per device, with
+// that device current); null on failure, with the error recorded.
+void *scratch_ptr(int device, int *rc) {
+    *rc = SC_OK;
+    if (device < 0 || device >= MAX_DEVICES) {
+        *rc = SC_ERR_UNSUPPORTED;
+        g_err = "device index beyond the library's static decode state table";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *rc = SC_ERR_HIP;
+            g_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+            return nullptr;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -495,6 +533,11 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     SC_HIP(hipGetDeviceCount(&n_dev), "hipGetDeviceCount");
     if (device < 0 || device >= n_dev) return fail(SC_ERR_ARG, "no such device");
     DeviceGuard guard(device);
+    {
+        // the static decode state of this device, resolved while it is current
+        int src = SC_OK;
+        if (!scratch_ptr(device, &src)) return src;
+    }
     sc_model *m = new sc_model();
     m->device = device;
     hipDeviceProp_t prop;
@@ -881,6 +924,30 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     DeviceGuard guard(m->device);
     DecState *state = (DecState *)workspace;
     int32_t *stat_dev = (int32_t *)((char *)workspace + dec_state_bytes(n_chunks));
+    return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
+                          state, stat_dev, as_stream(stream));
+}
+
+int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const int64_t *word_off,
+                                const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks, uint8_t *tokens,
+                                const int64_t *tok_off, int32_t *status, const int32_t *lengths_host,
+                                void *stream) {
+    if (!m || n_chunks < 0) return fail(SC_ERR_ARG, "bad argument");
+    if (n_chunks > SC_STATIC_DEC_MAX_CHUNKS)
+        return fail(SC_ERR_ARG, "sc_decompress_chunks_static decodes at most SC_STATIC_DEC_MAX_CHUNKS (" +
+                                    std::to_string(SC_STATIC_DEC_MAX_CHUNKS) + ") chunks per call; got " +
+                                    std::to_string(n_chunks));
+    if (n_chunks == 0) return SC_OK;
+    if (!words || !word_off || !word_cnt || !lengths || !tokens || !tok_off || !status)
+        return fail(SC_ERR_ARG, "null device pointer");
+    DeviceGuard guard(m->device);
+    int rc = SC_OK;
+    void *base = scratch_ptr(m->device, &rc);
+    if (!base) return rc;
+    // every DecState is written by a segment before a later one reads it and
+    // the statistics are written before they are read: nothing to clear
+    DecState *state = (DecState *)base;
+    int32_t *stat_dev = (int32_t *)((char *)base + SCRATCH_STATE_BYTES);
     return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
                           state, stat_dev, as_stream(stream));
 }
