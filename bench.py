@@ -1,36 +1,47 @@
 """SigComp codec benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c5|c1|c2|ceiling|coder]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c3|c5|c1|c2|ceiling|coder]
 
-Default workload (config c3+c4): 4,000 seeded synthetic R10.4.1-like reads
-(~80 M int16 samples), bundled lossless model, chunk_len 2048.  One step =
-one GPU compress of every chunk (teacher-forced MLP fused with the frequency
-step, then range encoder) followed by the GPU decompress of the resulting
-streams (persistent autoregressive decode of all chunks at once).  Inputs
-(token chunks / range-coded words) are resident in HBM before the timed
-region; host-side signal split and framing are outside it.
+Default (--config all): every BASELINE configuration in one JSON line.
 
-Prints one JSON line: value = round-trip Msamples/s (samples / (compress +
-decompress time)); compress and decompress rates, bits/sample, the
-roofline of the dominant kernel (k_decompress, int8 MFMA bound) measured
-with HIP events on its own stream, and the CPU oracle baseline on a bounded
-sample.  c5 = lossy (lsb 3, RNA-like reads, lossy model); c1 = the
-reference's CPU-runnable case (64 reads, lossless), with the CPU oracle run
-over the whole workload and every chunk's bytes compared; c2 = MLP
-microbenchmark (1,048,576 context rows -> int32 CDF tables); ceiling = the
-int8 MFMA rate the GPU sustains at its power limit (register-operand MFMA
-chains on every CU, random and zero operands), recorded in
-profiles/mfma_ceiling.txt and quoted beside the 5.0 POP/s spec peak;
-coder = the step-API coder kernels (logits -> CDF, encode step, decode
-step) timed as their own launches against HBM bandwidth.
+* headline = c3 + c4: 4,000 seeded synthetic R10.4.1-like reads (~82 M
+  int16 samples), bundled lossless model, chunk_len 2048.  One step = one GPU
+  compress of every chunk (teacher-forced MLP fused with the frequency step,
+  then the range encoder; c3) followed by the GPU decompress of the resulting
+  streams (persistent autoregressive decode of all chunks at once; c4).
+  Inputs (token chunks / range-coded words) are resident in HBM before the
+  timed region; host-side signal split and framing are outside it (the
+  PCIe-inclusive read pipeline is reported separately as end_to_end).
+  value = samples / (compress + decompress time), HIP events on the
+  launching stream; the roofline of the dominant kernel (k_decompress, int8
+  MFMA bound) and of k_compress_mlp; cpu_baseline = the C oracle (a
+  restatement of the reference CPU backend) on a bounded sample, run the way
+  the reference's CPU backend runs (all physical cores, 4,096-chunk decode
+  batches), plus a 1-thread figure;
+* configs.c1: the reference's CPU-runnable case (64 reads) on the GPU, and the
+  CPU oracle over the whole workload with every chunk's bytes compared;
+* configs.c2: MLP microbenchmark, 1,048,576 context rows -> int32 CDF tables,
+  seeded random per-channel model with the checkpoints' layer dims;
+* configs.c5: lossy (lsb 3, RNA-like reads, lossy model), same fields as the
+  headline;
+* power: socket power sampled every 20 ms by a separate process over each
+  timed region (average W and J per Msample).
+
+Single configurations (--config c3 / c5 / c1 / c2) are the runs the rocprofv3
+summaries under profiles/ were made from; ceiling = the int8 MFMA rate the
+GPU sustains at its power limit (profiles/mfma_ceiling.txt); coder = the
+step-API coder kernels timed as their own launches against HBM bandwidth.
 """
 
 from __future__ import annotations
 
 import argparse
+import glob
 import json
 import os
+import subprocess
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -43,11 +54,108 @@ OPS_PER_ROW = 2 * (8192 * 512 + 7 * 512 * 512 + 512 * 256)   # 12,320,768 int8 o
 PEAK_INT8_TOPS = 5000.0                                       # MI355X dense int8
 PEAK_HBM_GBS = 8000.0
 CHUNK_LEN = 2048
+METRIC = "compress/decompress Msamples/s on 1 MI355X; INT8 MFMA util; archive bits/sample"
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
+
+# ------------------------------------------------------------------ power
+
+_SAMPLER = r"""
+import sys, time
+path, period = sys.argv[1], float(sys.argv[2])
+f = open(path, "rb", buffering=0)
+out = sys.stdout
+while True:
+    f.seek(0)
+    v = f.read(64).strip()
+    out.write(f"{time.monotonic()} {int(v)}\n")
+    out.flush()
+    time.sleep(period)
+"""
+
+
+class PowerSampler:
+    """Socket power of GPU 0 sampled every `period` s by a separate process
+    (hwmon power1_input in uW, what `amd-smi metric -p` reports as socket
+    power); window(t0, t1) averages the samples of a time.monotonic()
+    interval.  Inactive (None results) where the sysfs file is absent."""
+
+    def __init__(self, period=0.02):
+        files = sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_input") +
+                       glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_average"))
+        self.path = files[0] if files else None
+        self.samples = []
+        self.proc = None
+        if self.path:
+            self.proc = subprocess.Popen([sys.executable, "-c", _SAMPLER, self.path, str(period)],
+                                         stdout=subprocess.PIPE, text=True)
+            self.thread = threading.Thread(target=self._read, daemon=True)
+            self.thread.start()
+
+    def _read(self):
+        for line in self.proc.stdout:
+            t, p = line.split()
+            self.samples.append((float(t), int(p) * 1e-6))
+
+    def window(self, t0, t1):
+        if not self.proc:
+            return None
+        time.sleep(0.05)   # let the last samples arrive
+        w = [p for t, p in list(self.samples) if t0 <= t <= t1]
+        return {"avg_w": round(float(np.mean(w)), 1), "max_w": round(float(np.max(w)), 1),
+                "samples": len(w)} if w else None
+
+    def stop(self):
+        if self.proc:
+            self.proc.terminate()
+            self.proc.wait(timeout=10)
+
+
+def power_fields(pw, seconds, samples):
+    """Average power over a timed region -> {avg_w, j_per_msample, ...}."""
+    if not pw:
+        return None
+    return {**pw, "j_per_msample": round(pw["avg_w"] * seconds / (samples / 1e6), 3),
+            "source": "hwmon power1_input of GPU 0 (socket power), sampled every 20 ms by a separate process "
+                      "over the timed steps"}
+
+
+# ---------------------------------------------------------- CPU hardware
+
+def physical_cores():
+    """Physical cores among the CPUs this process may run on: distinct
+    thread-sibling sets (the reference's default thread count,
+    cpu_runtime.py:37-80 / main.py:1763-1766)."""
+    cpus = sorted(os.sched_getaffinity(0))
+    sib = set()
+    for c in cpus:
+        try:
+            sib.add(Path(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list").read_text().strip())
+        except OSError:
+            return len(cpus)
+    return len(sib) or len(cpus)
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_hardware():
+    import oracle
+    return {"cpu_model": cpu_model(), "logical_cpus": len(os.sched_getaffinity(0)),
+            "physical_cores": physical_cores(), "int8_path": "AVX-512 VNNI" if oracle.uses_vnni() else "portable C"}
+
+
+# ------------------------------------------------------------- workloads
 
 def build_workload(cfg_name, n_reads):
     from sigcomp_amd import signal, synth
@@ -59,19 +167,35 @@ def build_workload(cfg_name, n_reads):
     return cfg, reads, samples, small, chunks
 
 
-def bench_codec(args):
+def model_path(cfg):
+    from sigcomp_amd.model_io import DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH
+    return DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy" else DEFAULT_QUANT_LOSSLESS_MODEL_PATH
+
+
+def roofline(kernel, tokens, seconds, config, direction):
+    achieved = tokens * OPS_PER_ROW / seconds / 1e12
+    return {"kernel": kernel, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "traffic": pmc_traffic(config, kernel),
+            "traffic_source": f"profiles/traffic_{config}.txt (rocprofv3 PMC, bytes per call)",
+            "algorithmic": f"{OPS_PER_ROW} int8 ops per {direction} token x {tokens} tokens per call",
+            **ceiling_fields(achieved), **pmc_mfma(config, kernel)}
+
+
+def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
+    """One configuration's GPU compress + decompress, timed with HIP events on
+    its own stream; every chunk round-trips, 24 random chunks' bytes are
+    compared with the CPU oracle.  -> (result dict, raw data for the CPU legs)."""
     import torch
     from sigcomp_amd import _hip
-    from sigcomp_amd.model_io import DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH
     from sigcomp_amd.quant_mlp_export import QuantMLPCompression
 
-    cfg, reads, samples, small, chunks = build_workload(args.config, args.n_reads)
-    model_path = DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy" else DEFAULT_QUANT_LOSSLESS_MODEL_PATH
-    codec = QuantMLPCompression(chunk_len=CHUNK_LEN, gpu=0, model_path=model_path)
+    cfg, reads, samples, small, chunks = build_workload(name, n_reads)
+    codec = QuantMLPCompression(chunk_len=CHUNK_LEN, gpu=0, model_path=model_path(cfg))
     n = len(chunks)
     lengths = np.array([len(c) for c in chunks], np.int32)
     n_tokens = int(lengths.sum())
-    log(f"[bench] {args.config}: {len(reads)} reads, {samples} samples, {n_tokens} tokens, {n} chunks")
+    log(f"[bench] {name}: {len(reads)} reads, {samples} samples, {n_tokens} tokens, {n} chunks")
     tok_off = np.zeros(n, np.int64)
     np.cumsum(lengths[:-1], out=tok_off[1:])
     cap = (lengths + 2).astype(np.int32)
@@ -87,6 +211,8 @@ def bench_codec(args):
     o_cnt = torch.empty(n, dtype=torch.int32, device=dev)
     out_tokens = torch.empty(n_tokens, dtype=torch.uint8, device=dev)
     dstatus = torch.empty(n, dtype=torch.int32, device=dev)
+    o_len_host = np.ascontiguousarray(lengths[order])
+    dws = codec._decompress_workspace(n)
     L = _hip.lib()
     stream = torch.cuda.Stream(device=dev)          # default priority
     h = codec.hip.handle
@@ -97,9 +223,6 @@ def bench_codec(args):
                                         _hip.ptr(cnt), _hip.ptr(status), _hip.ptr(ws), ws.numel(),
                                         stream.cuda_stream))
 
-    o_len_host = np.ascontiguousarray(lengths[order])
-    dws = codec._decompress_workspace(n)
-
     def decompress():
         torch.index_select(cnt, 0, o_idx, out=o_cnt)
         _hip.check(L.sc_decompress_chunks(h, _hip.ptr(words), _hip.ptr(o_woff), _hip.ptr(o_cnt),
@@ -107,24 +230,24 @@ def bench_codec(args):
                                           _hip.ptr(dstatus), o_len_host.ctypes.data, _hip.ptr(dws),
                                           dws.numel(), stream.cuda_stream))
 
-    if args.copy_mib:
+    if copy_mib:
         # one plain elementwise kernel moving a known number of bytes (read
         # copy_mib MiB, write copy_mib MiB), outside the timed region: the
         # reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters
-        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
     with torch.cuda.device(dev), torch.cuda.stream(stream):
-        for w in range(args.warmup):
+        for w in range(warmup):
             compress(); decompress()
             stream.synchronize()
-            log(f"[bench] warmup {w + 1}/{args.warmup} done")
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        log(f"[bench] {name}: {warmup} warmup steps done")
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(args.steps):
+        t0 = time.monotonic()
+        for k in range(steps):
             ev[k][0].record(stream)
             compress()
             ev[k][1].record(stream)
@@ -132,12 +255,12 @@ def bench_codec(args):
             ev[k][2].record(stream)
         stream.synchronize()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    t_c = np.mean([e[0].elapsed_time(e[1]) for e in ev]) / 1e3
-    t_d = np.mean([e[1].elapsed_time(e[2]) for e in ev]) / 1e3
+        t1 = time.monotonic()
+    wall = t1 - t0
+    t_c = float(np.mean([e[0].elapsed_time(e[1]) for e in ev])) / 1e3
+    t_d = float(np.mean([e[1].elapsed_time(e[2]) for e in ev])) / 1e3
     if int(status.sum().item()) or int(dstatus.sum().item()):
         raise RuntimeError("codec reported a stream error")
-    # parity: lossless round trip on every chunk; chunk bytes vs the CPU oracle on a sample
     back = out_tokens.cpu().numpy()
     if not np.array_equal(back, t_tokens.cpu().numpy()):
         raise RuntimeError("round trip mismatch")
@@ -145,54 +268,35 @@ def bench_codec(args):
     words_np = words.cpu().numpy().view(np.uint32)
     comp_bytes = int(cnt_np.sum()) * 4 + 2 * n
     parity = oracle_sample_check(codec.model, chunks, words_np, word_off, cnt_np)
-    e2e = end_to_end(codec, reads, cfg["lsb"])
-    log(f"[bench] compress {t_c * 1e3:.1f} ms, decompress {t_d * 1e3:.1f} ms, oracle sample ok={parity}")
-    rows = n_tokens
-    achieved = rows * OPS_PER_ROW / t_d / 1e12
+    log(f"[bench] {name}: compress {t_c * 1e3:.1f} ms, decompress {t_d * 1e3:.1f} ms, oracle sample ok={parity}")
     res = {
-        "metric": "compress/decompress Msamples/s on 1 MI355X; INT8 MFMA util; archive bits/sample",
-        "value": round(samples / (t_c + t_d) / 1e6, 3),
-        "unit": "Msamples/s (round trip)",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "workload": f"{name}: {len(reads)} reads, {samples} samples, {n} chunks of <= {CHUNK_LEN} tokens, "
+                    f"model {cfg['model']}, lsb {cfg['lsb']}",
+        "reads": len(reads), "samples": samples, "tokens": n_tokens, "chunks": n,
+        "round_trip_msamples_s": round(samples / (t_c + t_d) / 1e6, 3),
         "ms_per_step": round((t_c + t_d) * 1e3, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {"workload": f"{args.config}: {len(reads)} reads, {samples} samples, {n} chunks of "
-                               f"<= {CHUNK_LEN} tokens, model {cfg['model']}, lsb {cfg['lsb']}",
-                   "reads": len(reads), "samples": samples, "tokens": n_tokens, "chunks": n},
         "compress_msamples_s": round(samples / t_c / 1e6, 3),
         "decompress_msamples_s": round(samples / t_d / 1e6, 3),
+        "compress_ms": round(t_c * 1e3, 3), "decompress_ms": round(t_d * 1e3, 3),
         "bits_per_sample_tokens": round(comp_bytes * 8 / samples, 4),
-        "parity": {"round_trip": True, "oracle_sample_chunks": parity},
+        "parity": {"round_trip_all_chunks": True, "oracle_sample_chunks": parity},
         "wall_s_timed": round(wall, 3),
-        "end_to_end": e2e,
-        "roofline": {"kernel": "k_decompress", "bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                     "traffic": pmc_traffic(args.config, "k_decompress"),
-                     "traffic_source": f"profiles/traffic_{args.config}.txt (rocprofv3 PMC, bytes per launch)",
-                     "algorithmic": f"{OPS_PER_ROW} int8 ops per decoded token x {rows} tokens per launch",
-                     **ceiling_fields(achieved), **pmc_mfma(args.config, "k_decompress")},
-        # the other half of the round trip, same fields (the compress call:
-        # k_tile_scan, k_tile_table, k_compress_mlp, k_encode_pairs)
-        "roofline_compress": {"kernel": "k_compress_mlp", "bound": "mfma",
-                              "achieved": round(rows * OPS_PER_ROW / t_c / 1e12, 2), "peak": PEAK_INT8_TOPS,
-                              "unit": "TFLOP/s",
-                              "frac": round(rows * OPS_PER_ROW / t_c / 1e12 / PEAK_INT8_TOPS, 4),
-                              "traffic": pmc_traffic(args.config, "k_compress_mlp"),
-                              "algorithmic": f"{OPS_PER_ROW} int8 ops per coded token x {rows} tokens per launch",
-                              **ceiling_fields(rows * OPS_PER_ROW / t_c / 1e12),
-                              **pmc_mfma(args.config, "k_compress_mlp")},
+        "power": power_fields(sampler.window(t0, t1), t_c + t_d, samples),
+        "roofline": roofline("k_decompress", n_tokens, t_d, name, "decoded"),
+        "roofline_compress": roofline("k_compress_mlp", n_tokens, t_c, name, "coded"),
     }
-    return res, chunks, samples, cfg, (words_np, word_off, cnt_np)
+    if e2e:
+        res["end_to_end"] = end_to_end(codec, reads, cfg["lsb"])
+    return res, dict(model=codec.model, chunks=chunks, samples=samples, words=words_np, word_off=word_off,
+                     word_cnt=cnt_np)
 
 
 def end_to_end(codec, reads, lsb):
-    """One untimed-by-`value` pass of the whole read pipeline as main.py
-    drives it: int16 reads in host memory -> split (host library) ->
-    batch_inference_reads (host->device copy, GPU compress, framing) ->
-    batch_inference_reads back (parsing, GPU decompress, device->host) ->
-    reassembly.  Reports the PCIe-inclusive rate and the stage times."""
+    """One pass of the whole read pipeline as main.py drives it: int16 reads
+    in host memory -> split (host library) -> batch_inference_reads (host ->
+    device copy, GPU compress, framing) -> batch_inference_reads back
+    (parsing, GPU decompress, device -> host) -> reassembly.  Reports the
+    PCIe-inclusive rate and the stage times (not the headline value)."""
     from sigcomp_amd import signal
     t = {}
     t0 = time.perf_counter()
@@ -223,7 +327,7 @@ def end_to_end(codec, reads, lsb):
 
 
 def pmc_traffic(config, kernel):
-    """HBM-side bytes per launch of `kernel` from the committed rocprofv3 PMC
+    """HBM-side bytes per call of `kernel` from the committed rocprofv3 PMC
     summary of this workload (profiles/traffic_<config>.txt: FETCH_SIZE +
     WRITE_SIZE passes, calibrated against a copy kernel), or None."""
     path = REPO / "profiles" / f"traffic_{config}.txt"
@@ -270,68 +374,83 @@ def oracle_sample_check(model, chunks, words_np, word_off, cnt_np, k=24):
     return int(len(idx))
 
 
-def cpu_baseline(model, chunks, gpu_words, word_off, word_cnt, samples_per_token,
-                 n_compress=None, n_decode=512, decode_prefix=256):
-    """CPU oracle (C restatement of the reference CPU backend) on a bounded
-    sample of the same workload, all host threads:
+# ------------------------------------------------------------ CPU legs
 
-    * compress: 18 x threads random whole chunks (teacher-forced MLP batched
-      over each chunk, as CPUQuantMLPCompression.compress_chunks does);
-    * decompress: the first `decode_prefix` tokens of `n_decode` random
-      chunks decoded together, autoregressively, batched across chunks
-      (as CPUQuantMLPCompression.decompress_chunks batches up to 4,096);
-      the streams are the GPU's words, bit-identical to the oracle's.
-    Rates are converted to samples with the workload's samples per token;
-    the whole sample takes about 15 s on 16 host threads."""
-    sys.path.insert(0, str(REPO / "oracle"))
+def _cpu_leg(om, chunks, words, word_off, word_cnt, threads, n_compress, n_decode, prefix, rng):
+    """Compress n_compress random whole chunks; decode the first `prefix`
+    tokens of n_decode random chunks in one batch (autoregressive, batched
+    across chunks); check the decode against the tokens.  -> token counts
+    and seconds."""
     import oracle
-    threads = oracle.cpu_count()
     oracle.set_num_threads(threads)
-    om = oracle.OracleModel(model)
-    rng = np.random.default_rng(1)
-    n_compress = n_compress or 18 * threads
     pick = rng.choice(len(chunks), size=min(len(chunks), n_compress), replace=False)
     sample = [chunks[i] for i in pick]
     t0 = time.perf_counter()
     oracle.compress_chunks(om, sample)
     tc = time.perf_counter() - t0
-    ctoks = sum(len(c) for c in sample)
     dpick = rng.choice(len(chunks), size=min(len(chunks), n_decode), replace=False)
-    streams = [gpu_words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in dpick]
-    lens = [min(decode_prefix, len(chunks[i])) for i in dpick]
+    streams = [words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in dpick]
+    lens = [min(prefix, len(chunks[i])) for i in dpick]
     t0 = time.perf_counter()
     dec = oracle.decompress_chunks(om, streams, lens)
     td = time.perf_counter() - t0
-    for i, d in zip(dpick, dec):
-        if not np.array_equal(d, chunks[i][:len(d)]):
+    for i, dd in zip(dpick, dec):
+        if not np.array_equal(dd, chunks[i][:len(dd)]):
             raise RuntimeError("CPU oracle decode disagrees with the GPU stream")
-    dtoks = sum(lens)
-    c_rate = ctoks * samples_per_token / tc
-    d_rate = dtoks * samples_per_token / td
-    return {"value": round(1.0 / (1.0 / c_rate + 1.0 / d_rate) / 1e6, 5),
-            "unit": "Msamples/s (round trip)", "cores": threads, "kind": "port",
-            "compress_msamples_s": round(c_rate / 1e6, 5),
-            "decompress_msamples_s": round(d_rate / 1e6, 5),
-            "sample": f"compress: {len(sample)} random whole chunks ({ctoks} tokens, {tc:.1f} s); "
-                      f"decompress: first {decode_prefix} tokens of {len(dpick)} random chunks decoded "
-                      f"together ({dtoks} tokens, {td:.1f} s); C oracle on {threads} threads"}
+    return sum(len(c) for c in sample), tc, sum(lens), td
 
 
-def cpu_full(model, chunks, gpu_words, word_off, word_cnt, samples):
-    """Config c1 (the reference's CPU-runnable case): the CPU oracle over the
-    whole workload, all host threads, and every chunk checked.  Compress:
-    every chunk, bytes compared with the GPU's; decompress: every GPU stream
-    decoded autoregressively, batched across chunks, tokens compared with
-    the originals.  About a minute on 16 host threads."""
+def cpu_baseline(raw, hw):
+    """The C oracle (restatement of the reference CPU backend) on a bounded
+    sample of the workload, as the reference's CPU backend runs: one thread
+    per physical core (main.py:1763-1766), chunks compressed independently,
+    decode batched over 4,096 chunks (the reference's --cpu-batch-size
+    default for decompress, main.py:1958-1961), int8 dot products with
+    AVX-512 VNNI where the host has it (the reference's int_mm backend,
+    cpu_int_inference.py:24-82).  Also one thread on a smaller sample.
+    Rates are converted to samples with the workload's samples per token."""
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
-    threads = oracle.cpu_count()
+    om = oracle.OracleModel(raw["model"])
+    spt = raw["samples"] / sum(len(c) for c in raw["chunks"])
+    threads = hw["physical_cores"]
+    rng = np.random.default_rng(1)
+    args = (om, raw["chunks"], raw["words"], raw["word_off"], raw["word_cnt"])
+    ct, tc, dt, td = _cpu_leg(*args, threads, 64 * threads, 4096, 384, rng)
+    ct1, tc1, dt1, td1 = _cpu_leg(*args, 1, 12, 256, 96, rng)
     oracle.set_num_threads(threads)
-    om = oracle.OracleModel(model)
+    c_rate, d_rate = ct * spt / tc, dt * spt / td
+    c1r, d1r = ct1 * spt / tc1, dt1 * spt / td1
+    rt = lambda c, d: 1.0 / (1.0 / c + 1.0 / d)
+    return {"value": round(rt(c_rate, d_rate) / 1e6, 5), "unit": "Msamples/s (round trip)", "cores": threads,
+            "kind": "port",
+            "compress_msamples_s": round(c_rate / 1e6, 5), "decompress_msamples_s": round(d_rate / 1e6, 5),
+            "one_thread": {"value": round(rt(c1r, d1r) / 1e6, 6), "compress_msamples_s": round(c1r / 1e6, 6),
+                           "decompress_msamples_s": round(d1r / 1e6, 6)},
+            **hw,
+            "sample": f"{threads} threads: compress {64 * threads} random whole chunks ({ct} tokens, {tc:.1f} s); "
+                      f"decompress the first 384 tokens of 4096 random chunks decoded together ({dt} tokens, "
+                      f"{td:.1f} s); 1 thread: 12 whole chunks ({tc1:.1f} s), first 96 tokens of 256 chunks "
+                      f"({td1:.1f} s); C oracle, the GPU's streams decoded and checked"}
+
+
+def cpu_full(raw, hw):
+    """Config c1 (the reference's CPU-runnable case): the CPU oracle over the
+    whole workload, one thread per physical core, every chunk checked:
+    compress every chunk (bytes compared with the GPU's), decode every GPU
+    stream in one batch (all 675 chunks fit the reference's 4,096-chunk
+    batch), tokens compared with the originals."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    threads = hw["physical_cores"]
+    oracle.set_num_threads(threads)
+    om = oracle.OracleModel(raw["model"])
+    chunks, samples = raw["chunks"], raw["samples"]
     t0 = time.perf_counter()
     ref = oracle.compress_chunks(om, chunks)
     tc = time.perf_counter() - t0
-    streams = [gpu_words[word_off[i]:word_off[i] + word_cnt[i]].tobytes() for i in range(len(chunks))]
+    w, wo, wc = raw["words"], raw["word_off"], raw["word_cnt"]
+    streams = [w[wo[i]:wo[i] + wc[i]].tobytes() for i in range(len(chunks))]
     bad = [i for i in range(len(chunks)) if streams[i] != ref[i]]
     if bad:
         raise RuntimeError(f"{len(bad)} chunks differ from the CPU oracle (first {bad[0]})")
@@ -340,24 +459,25 @@ def cpu_full(model, chunks, gpu_words, word_off, word_cnt, samples):
     td = time.perf_counter() - t0
     if not all(np.array_equal(d, c) for d, c in zip(dec, chunks)):
         raise RuntimeError("CPU oracle decode disagrees with the GPU streams")
-    c_rate, d_rate = samples / tc, samples / td
-    return {"value": round(samples / (tc + td) / 1e6, 5),
-            "unit": "Msamples/s (round trip)", "cores": threads, "kind": "port",
-            "compress_msamples_s": round(c_rate / 1e6, 5),
-            "decompress_msamples_s": round(d_rate / 1e6, 5),
-            "sample": f"the whole workload: {len(chunks)} chunks compressed ({tc:.1f} s) and decoded "
-                      f"({td:.1f} s) by the C oracle on {threads} threads; all {len(chunks)} chunk byte "
-                      f"strings equal the GPU's"}
+    return {"value": round(samples / (tc + td) / 1e6, 5), "unit": "Msamples/s (round trip)", "cores": threads,
+            "kind": "port",
+            "compress_msamples_s": round(samples / tc / 1e6, 5),
+            "decompress_msamples_s": round(samples / td / 1e6, 5), **hw,
+            "sample": f"the whole workload: {len(chunks)} chunks compressed ({tc:.1f} s) and decoded in one batch "
+                      f"({td:.1f} s) by the C oracle on {threads} threads; all {len(chunks)} chunk byte strings "
+                      f"equal the GPU's"}
 
 
-def bench_mlp(args):
-    """Config c2: 1,048,576 context rows -> int32 CDF tables, seeded random
-    per-channel model with the bundled checkpoints' layer dims."""
+# ----------------------------------------------------------------- c2
+
+def run_mlp(rows, steps, warmup, sampler):
+    """Config c2: `rows` context rows -> int32 CDF tables, seeded random
+    per-channel model with the bundled checkpoints' layer dims; 256 random
+    rows checked against the oracle."""
     import torch
     from sigcomp_amd import signal, synth
     from sigcomp_amd.model_io import random_int_model
     from sigcomp_amd.quant_mlp_export import HipModel
-    rows = args.rows
     m = random_int_model(seed=2, per_channel=True)
     hm = HipModel(m, torch.device("cuda:0"))
     toks = np.concatenate([signal.split_signal(r)[1] for r in synth.synth_reads(64, 202, synth.DNA)])
@@ -366,16 +486,18 @@ def bench_mlp(args):
     idx = starts[:, None] + np.arange(64)[None, :]
     ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
     ctx_d = torch.from_numpy(ctx).cuda()
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         hm.forward_windows(ctx_d, "cdf")
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.monotonic()
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = hm.forward_windows(ctx_d, "cdf")
     e1.record()
     torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / 1e3 / args.steps
+    t1 = time.monotonic()
+    t = e0.elapsed_time(e1) / 1e3 / steps
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
     sub = np.random.default_rng(4).choice(rows, 256, replace=False)
@@ -384,16 +506,28 @@ def bench_mlp(args):
     if not np.array_equal(out[torch.from_numpy(sub).cuda()].cpu().numpy().astype(np.int64), ref):
         raise RuntimeError("c2 CDF mismatch vs oracle")
     achieved = rows * OPS_PER_ROW / t / 1e12
-    return {"metric": "INT8 MLP rows/s -> int32 CDF (c2 microbench)", "value": round(rows / t / 1e6, 3),
-            "unit": "Mrows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "ms_per_step": round(t * 1e3, 3), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-            "config": {"workload": f"c2: {rows} context rows, random per-channel int8 model"},
+    pw = sampler.window(t0, t1) if sampler else None
+    return {"workload": f"c2: {rows} context rows -> int32 CDF tables, random per-channel int8 model with the "
+                        "checkpoints' layer dims",
+            "mrows_s": round(rows / t / 1e6, 3), "ms_per_step": round(t * 1e3, 3), "steps": steps,
+            "parity": {"oracle_rows": 256},
+            "power": ({**pw, "j_per_mrow": round(pw["avg_w"] * t / (rows / 1e6), 3)} if pw else None),
             "roofline": {"kernel": "k_mlp_context<cdf>", "bound": "mfma", "achieved": round(achieved, 2),
-                         "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                         "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                         "traffic": None,
+                         "algorithmic": f"{OPS_PER_ROW} int8 ops per row x {rows} rows per launch",
                          **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")}}
 
+
+def bench_mlp(args):
+    r = run_mlp(args.rows, args.steps, args.warmup, None)
+    return {"metric": "INT8 MLP rows/s -> int32 CDF (c2 microbench)", "value": r["mrows_s"], "unit": "Mrows/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic", "config": {"workload": r["workload"]}, "roofline": r["roofline"]}
+
+
+# ------------------------------------------------------- ceiling, coder
 
 def bench_ceiling(args):
     """The int8 MFMA rate the GPU sustains at its power limit: every CU runs
@@ -401,8 +535,6 @@ def bench_ceiling(args):
     about 6 s per operand set (long enough for the power controller to settle)
     with random int8 operands (the data the codec's MFMAs see) and with
     zeros (no toggling: close to the clock-limited 5.0 POP/s)."""
-    import time
-
     import torch
     from sigcomp_amd import _hip
     L = _hip.lib()
@@ -455,14 +587,14 @@ CODER_BYTES = {"k_logits_to_cdf": 256 + 257 * 8, "k_encode_step": 256 + 8 + 8 + 
 
 
 def bench_coder(args):
-    """The reference's step-API coder kernels timed as
-    their own launches, HIP events on the launching stream: B streams of
-    synthetic int8 logits per step (normal, sd 20; the coded symbol is the
-    argmax of the logits plus uniform noise), `steps` steps, called through
-    the C ABI.  At B = 1,048,576 one step's logits (268 MB) exceed the 256 MB
-    MALL, so the launches stream from HBM; B = 20,480 (the reference's batch)
-    shows the launch-bound regime.  The decoder, fed the encoder's sealed
-    words, must return every coded symbol."""
+    """The reference's step-API coder kernels (logits -> CDF, encode step,
+    decode step) timed as their own launches, HIP events on the launching
+    stream: B streams of synthetic int8 logits per step (normal, sd 20; the
+    coded symbol is the argmax of the logits plus uniform noise), `steps`
+    steps, called through the C ABI.  At B = 1,048,576 one step's logits
+    (268 MB) exceed the 256 MB MALL, so the launches stream from HBM;
+    B = 20,480 (the reference's batch) shows the launch-bound regime.  The
+    decoder, fed the encoder's sealed words, must return every coded symbol."""
     import torch
     from sigcomp_amd import _hip
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
@@ -560,12 +692,83 @@ def ceiling_fields(achieved):
             "power_capped_peak_source": "profiles/mfma_ceiling.txt (bench.py --config ceiling)"}
 
 
+# ----------------------------------------------------------------- main
+
+def headline(res, steps, warmup):
+    """The contract's fields for one codec configuration's result."""
+    return {"metric": METRIC, "value": res["round_trip_msamples_s"], "unit": "Msamples/s (round trip)",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic",
+            "config": {"workload": res["workload"], "reads": res["reads"], "samples": res["samples"],
+                       "tokens": res["tokens"], "chunks": res["chunks"]}}
+
+
+def run_all(args):
+    """Every BASELINE configuration, one JSON line (headline = c3 + c4)."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    sampler = PowerSampler()
+    try:
+        hw = cpu_hardware()
+        c3, raw3 = run_codec("c3", args.steps, args.warmup, sampler, copy_mib=args.copy_mib)
+        out = headline(c3, args.steps, args.warmup)
+        out.update({k: c3[k] for k in ("compress_msamples_s", "decompress_msamples_s", "bits_per_sample_tokens",
+                                        "parity", "wall_s_timed", "power", "end_to_end", "roofline",
+                                        "roofline_compress")})
+        c5, raw5 = run_codec("c5", args.steps, args.warmup, sampler, e2e=False)
+        c1, raw1 = run_codec("c1", args.steps, args.warmup, sampler, e2e=False)
+        # c2 steps are ~5 ms: enough of them for a power reading of ~2 s
+        c2 = run_mlp(args.rows, max(args.steps, 400), args.warmup, sampler)
+        if not args.no_cpu_baseline:
+            log("[bench] cpu baselines ...")
+            out["cpu_baseline"] = cpu_baseline(raw3, hw)
+            c5["cpu_baseline"] = cpu_baseline(raw5, hw)
+            c1["cpu_baseline"] = cpu_full(raw1, hw)
+            c1["parity"]["oracle_all_chunks"] = len(raw1["chunks"])
+        keep = ("workload", "samples", "tokens", "chunks", "bits_per_sample_tokens", "power")
+        out["configs"] = {
+            "c1": c1,
+            "c2": c2,
+            "c3": {**{k: c3[k] for k in keep}, "compress_msamples_s": c3["compress_msamples_s"],
+                   "compress_ms": c3["compress_ms"], "roofline": c3["roofline_compress"],
+                   "note": "the headline's compress half"},
+            "c4": {**{k: c3[k] for k in keep}, "decompress_msamples_s": c3["decompress_msamples_s"],
+                   "decompress_ms": c3["decompress_ms"], "roofline": c3["roofline"],
+                   "note": "the headline's decompress half (the c3 archive's streams)"},
+            "c5": c5,
+        }
+        return out
+    finally:
+        sampler.stop()
+
+
+def run_one(args):
+    """One codec configuration (profiling runs)."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    sampler = PowerSampler()
+    try:
+        res, raw = run_codec(args.config, args.steps, args.warmup, sampler, n_reads=args.n_reads,
+                             e2e=args.config == "c3", copy_mib=args.copy_mib)
+    finally:
+        sampler.stop()
+    out = headline(res, args.steps, args.warmup)
+    out.update({k: v for k, v in res.items() if k not in out and k not in ("workload", "reads", "samples",
+                                                                             "tokens", "chunks")})
+    if not args.no_cpu_baseline:
+        hw = cpu_hardware()
+        if args.config == "c1":
+            out["cpu_baseline"] = cpu_full(raw, hw)
+        else:
+            out["cpu_baseline"] = cpu_baseline(raw, hw)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=["c3", "c5", "c1", "c2", "ceiling", "coder"])
+    ap.add_argument("--config", default="all", choices=["all", "c3", "c5", "c1", "c2", "ceiling", "coder"])
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -576,27 +779,8 @@ def main():
         print("bench.py measures one GPU only: the codec shards by independent reads with no "
               "collective, so multi-GPU runs are out of scope for this build", file=sys.stderr)
         sys.exit(2)
-    if args.config == "c2":
-        print(json.dumps(bench_mlp(args)), flush=True)
-        return
-    if args.config == "ceiling":
-        print(json.dumps(bench_ceiling(args)), flush=True)
-        return
-    if args.config == "coder":
-        print(json.dumps(bench_coder(args)), flush=True)
-        return
-    res, chunks, samples, cfg, gpu_out = bench_codec(args)
-    if not args.no_cpu_baseline:
-        from sigcomp_amd.model_io import load_int_model, DEFAULT_QUANT_LOSSY_MODEL_PATH, DEFAULT_QUANT_LOSSLESS_MODEL_PATH
-        model = load_int_model(DEFAULT_QUANT_LOSSY_MODEL_PATH if cfg["model"] == "lossy"
-                               else DEFAULT_QUANT_LOSSLESS_MODEL_PATH)
-        log("[bench] cpu baseline ...")
-        if args.config == "c1":
-            res["cpu_baseline"] = cpu_full(model, chunks, *gpu_out, samples)
-            res["parity"]["oracle_all_chunks"] = len(chunks)
-        else:
-            res["cpu_baseline"] = cpu_baseline(model, chunks, *gpu_out, samples / res["config"]["tokens"])
-    print(json.dumps(res), flush=True)
+    runners = {"all": run_all, "c2": bench_mlp, "ceiling": bench_ceiling, "coder": bench_coder}
+    print(json.dumps(runners.get(args.config, run_one)(args)), flush=True)
 
 
 if __name__ == "__main__":

@@ -95,6 +95,7 @@ def lib():
         L.sco_decompress_chunks.argtypes = [ctypes.POINTER(_Model), _i64p, _u32p, _i64p,
                                             _i32p, _i32p, ctypes.c_int64, _u8p, _i64p, _i32p]
         L.sco_num_threads.restype = ctypes.c_int
+        L.sco_uses_vnni.restype = ctypes.c_int
         L.sco_set_num_threads.argtypes = [ctypes.c_int]
         _LIB = L
     return _LIB
@@ -106,6 +107,13 @@ def set_num_threads(n: int) -> None:
 
 def num_threads() -> int:
     return int(lib().sco_num_threads())
+
+
+def uses_vnni() -> bool:
+    """True when the MLP runs its AVX-512 VNNI dot products (the int_mm
+    backend's instructions); SCO_NO_VNNI=1 in the environment before the
+    first call selects the portable C path."""
+    return bool(lib().sco_uses_vnni())
 
 
 class OracleModel:

@@ -16,6 +16,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -102,8 +105,9 @@ static inline void sco_dot4(const int8_t *x0, const int8_t *x1, const int8_t *x2
 }
 
 /* One quantised linear layer on `rows` activations (cpu_int_inference.py
- * :125-256 CPUBitExactInt8Linear; quant_mlp_export.py:21-76 on the GPU). */
-static void sco_linear_rows(const int8_t *x, int64_t rows, const sco_layer *L, int8_t *out)
+ * :125-256 CPUBitExactInt8Linear; quant_mlp_export.py:21-76 on the GPU),
+ * portable C. */
+static void sco_linear_rows_c(const int8_t *x, int64_t rows, const sco_layer *L, int8_t *out)
 {
     const int32_t k = L->k, n = L->n;
     int64_t r = 0;
@@ -124,16 +128,110 @@ static void sco_linear_rows(const int8_t *x, int64_t rows, const sco_layer *L, i
                                          L->bias[j], L->m0[j], L->shift[j], L->relu);
 }
 
+#if defined(__x86_64__)
+/* The same layer with AVX-512 VNNI, as the reference's int_mm backend runs on
+ * such hosts (oneDNN u8 x s8 dot products, cpu_int_inference.py:24-82):
+ * vpdpbusd multiplies unsigned by signed bytes, so each activation byte is
+ * offset by 128 (x ^ 0x80 = x + 128 as u8) and 128 * sum(w) is taken off
+ * again.  Exact: |sum| < 2**31 for k <= 65536, so the int32 accumulators
+ * never wrap, and the int32 result equals the wrapping sum of cpu_int_kernels.
+ * k must be a multiple of 64; wsum[j] = sum of weight row j. */
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static void sco_linear_rows_vnni(const int8_t *x, int64_t rows, const sco_layer *L, const int32_t *wsum,
+                                 int8_t *out)
+{
+    const int32_t k = L->k, n = L->n;
+    const __m512i flip = _mm512_set1_epi8((char)0x80);
+    int64_t r = 0;
+    for (; r < rows; r += 4) {
+        const int nr = rows - r < 4 ? (int)(rows - r) : 4;
+        const int8_t *xr[4];
+        for (int q = 0; q < 4; ++q) xr[q] = x + (r + (q < nr ? q : 0)) * k;
+        for (int32_t j = 0; j + 1 < n; j += 2) {
+            const int8_t *w0 = L->w + (int64_t)j * k, *w1 = w0 + k;
+            __m512i a[4][2];
+            for (int q = 0; q < 4; ++q) a[q][0] = a[q][1] = _mm512_setzero_si512();
+            for (int32_t i = 0; i < k; i += 64) {
+                const __m512i b0 = _mm512_loadu_si512((const void *)(w0 + i));
+                const __m512i b1 = _mm512_loadu_si512((const void *)(w1 + i));
+                for (int q = 0; q < 4; ++q) {
+                    const __m512i xv = _mm512_xor_si512(_mm512_loadu_si512((const void *)(xr[q] + i)), flip);
+                    a[q][0] = _mm512_dpbusd_epi32(a[q][0], xv, b0);
+                    a[q][1] = _mm512_dpbusd_epi32(a[q][1], xv, b1);
+                }
+            }
+            for (int q = 0; q < nr; ++q)
+                for (int h = 0; h < 2; ++h) {
+                    const int32_t acc = _mm512_reduce_add_epi32(a[q][h]) - 128 * wsum[j + h];
+                    out[(r + q) * n + j + h] = sco_requant(acc, L->bias[j + h], L->m0[j + h], L->shift[j + h],
+                                                           L->relu);
+                }
+        }
+        if (n & 1) {
+            const int32_t j = n - 1;
+            for (int q = 0; q < nr; ++q)
+                out[(r + q) * n + j] = sco_requant((int32_t)sco_dot(xr[q], L->w + (int64_t)j * k, k), L->bias[j],
+                                                   L->m0[j], L->shift[j], L->relu);
+        }
+    }
+}
+#endif
+
+int sco_num_threads(void);
+
+/* 1 when the VNNI path runs (x86-64 host with AVX-512 VNNI, and
+ * SCO_NO_VNNI unset or 0). */
+int sco_uses_vnni(void)
+{
+#if defined(__x86_64__)
+    static int state = -1;
+    if (state < 0) {
+        const char *e = getenv("SCO_NO_VNNI");
+        __builtin_cpu_init();
+        state = (!e || e[0] == '0') && __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw");
+    }
+    return state;
+#else
+    return 0;
+#endif
+}
+
+/* Weight row sums of a layer (for the VNNI offset), malloc'ed. */
+static int32_t *sco_row_sums(const sco_layer *L)
+{
+    int32_t *ws = (int32_t *)malloc(sizeof(int32_t) * (size_t)L->n);
+    for (int32_t j = 0; j < L->n; ++j) {
+        int32_t t = 0;
+        for (int32_t i = 0; i < L->k; ++i) t += L->w[(int64_t)j * L->k + i];
+        ws[j] = t;
+    }
+    return ws;
+}
+
+static void sco_linear_rows(const int8_t *x, int64_t rows, const sco_layer *L, const int32_t *wsum, int8_t *out)
+{
+#if defined(__x86_64__)
+    if (wsum && L->k % 64 == 0) {
+        sco_linear_rows_vnni(x, rows, L, wsum, out);
+        return;
+    }
+#endif
+    (void)wsum;
+    sco_linear_rows_c(x, rows, L, out);
+}
+
 void sco_linear(const int8_t *x, int64_t rows, int32_t k, const int8_t *w, int32_t n,
                 const int32_t *bias, const int64_t *m0, const int32_t *shift, int32_t relu,
                 int8_t *out)
 {
     sco_layer L = {n, k, w, bias, m0, shift, relu};
+    int32_t *wsum = sco_uses_vnni() ? sco_row_sums(&L) : NULL;
 #pragma omp parallel for schedule(static)
     for (int64_t r0 = 0; r0 < rows; r0 += SCO_ROW_BLOCK) {
         int64_t cnt = rows - r0 < SCO_ROW_BLOCK ? rows - r0 : SCO_ROW_BLOCK;
-        sco_linear_rows(x + r0 * k, cnt, &L, out + r0 * n);
+        sco_linear_rows(x + r0 * k, cnt, &L, wsum, out + r0 * n);
     }
+    free(wsum);
 }
 
 /* Embedding gather of a token window into one flat activation row,
@@ -161,7 +259,7 @@ static int64_t sco_max_width(const sco_model *M)
 /* Forward pass over up to SCO_ROW_BLOCK rows whose windows are given
  * explicitly (GPUBitExactMLPDecoder._ar_step, quant_mlp_export.py:133-138;
  * CPUBitExactMLPDecoder._ar_step, cpu_int_inference.py:323-343). */
-static int sco_mlp_block(const sco_model *M, const int32_t *ctx, int64_t rows,
+static int sco_mlp_block(const sco_model *M, int32_t *const *wsum, const int32_t *ctx, int64_t rows,
                          int8_t *buf0, int8_t *buf1, int8_t *logits)
 {
     const int64_t in_w = (int64_t)M->window * M->emb_dim;
@@ -172,7 +270,7 @@ static int sco_mlp_block(const sco_model *M, const int32_t *ctx, int64_t rows,
     int8_t *src = buf0, *dst = buf1;
     for (int i = 0; i < M->n_layers; ++i) {
         const int last = i == M->n_layers - 1;
-        sco_linear_rows(src, rows, &M->layers[i], last ? logits : dst);
+        sco_linear_rows(src, rows, &M->layers[i], wsum ? wsum[i] : NULL, last ? logits : dst);
         if (!last) { int8_t *t = src; src = dst; dst = t; }
     }
     return SCO_OK;
@@ -184,14 +282,23 @@ int sco_mlp_forward(const sco_model *M, const int32_t *ctx, int64_t rows, int8_t
     const int64_t wmax = sco_max_width(M);
     const int32_t n_out = M->layers[M->n_layers - 1].n;
     int status = SCO_OK;
+    int32_t *wsum[SCO_MAX_LAYERS];
+    const int vnni = sco_uses_vnni();
+    for (int i = 0; i < M->n_layers; ++i) wsum[i] = vnni ? sco_row_sums(&M->layers[i]) : NULL;
+    /* row blocks of at most SCO_ROW_BLOCK, small enough that every thread
+     * gets about two (batches of a few hundred rows keep all threads busy) */
+    int64_t blk = (rows + 2 * (int64_t)sco_num_threads() - 1) / (2 * (int64_t)sco_num_threads());
+    blk = (blk + 3) / 4 * 4;
+    if (blk < 4) blk = 4;
+    if (blk > SCO_ROW_BLOCK) blk = SCO_ROW_BLOCK;
 #pragma omp parallel
     {
         int8_t *b0 = (int8_t *)malloc((size_t)(SCO_ROW_BLOCK * wmax));
         int8_t *b1 = (int8_t *)malloc((size_t)(SCO_ROW_BLOCK * wmax));
 #pragma omp for schedule(dynamic, 1)
-        for (int64_t r0 = 0; r0 < rows; r0 += SCO_ROW_BLOCK) {
-            int64_t cnt = rows - r0 < SCO_ROW_BLOCK ? rows - r0 : SCO_ROW_BLOCK;
-            int st = sco_mlp_block(M, ctx + r0 * M->window, cnt, b0, b1, logits + r0 * n_out);
+        for (int64_t r0 = 0; r0 < rows; r0 += blk) {
+            int64_t cnt = rows - r0 < blk ? rows - r0 : blk;
+            int st = sco_mlp_block(M, vnni ? wsum : NULL, ctx + r0 * M->window, cnt, b0, b1, logits + r0 * n_out);
             if (st) {
 #pragma omp atomic write
                 status = st;
@@ -200,6 +307,7 @@ int sco_mlp_forward(const sco_model *M, const int32_t *ctx, int64_t rows, int8_t
         free(b0);
         free(b1);
     }
+    for (int i = 0; i < M->n_layers; ++i) free(wsum[i]);
     return status;
 }
 
@@ -435,9 +543,9 @@ static inline int32_t sco_window_token(const uint8_t *tokens, int64_t t, int32_t
 /* Compress one chunk: teacher-forced MLP over every step, then the range
  * encoder and seal (CPUQuantMLPCompression.compress_chunks,
  * cpu_compression.py:178-257). */
-static int sco_compress_one(const sco_model *M, const int64_t *lut, const uint8_t *tokens,
-                            int64_t length, uint32_t *out, int64_t cap, int64_t *n_words,
-                            int32_t *ctx, int8_t *b0, int8_t *b1, int8_t *logits)
+static int sco_compress_one(const sco_model *M, int32_t *const *wsum, const int64_t *lut,
+                            const uint8_t *tokens, int64_t length, uint32_t *out, int64_t cap,
+                            int64_t *n_words, int32_t *ctx, int8_t *b0, int8_t *b1, int8_t *logits)
 {
     const int32_t sos = M->emb_rows - 1;
     sco_enc e;
@@ -447,7 +555,7 @@ static int sco_compress_one(const sco_model *M, const int64_t *lut, const uint8_
         for (int64_t r = 0; r < cnt; ++r)
             for (int32_t p = 0; p < M->window; ++p)
                 ctx[r * M->window + p] = sco_window_token(tokens, t0 + r, p, M->window, sos);
-        int st = sco_mlp_block(M, ctx, cnt, b0, b1, logits);
+        int st = sco_mlp_block(M, wsum, ctx, cnt, b0, b1, logits);
         if (st) return st;
         for (int64_t r = 0; r < cnt; ++r) {
             st = sco_enc_symbol(&e, logits + r * SCO_VOCAB, lut, tokens[t0 + r], out, cap);
@@ -470,6 +578,9 @@ int sco_compress_chunks(const sco_model *M, const int64_t *lut, const uint8_t *t
 {
     const int64_t wmax = sco_max_width(M);
     int result = SCO_OK;
+    int32_t *wsum[SCO_MAX_LAYERS];
+    const int vnni = sco_uses_vnni();
+    for (int i = 0; i < M->n_layers; ++i) wsum[i] = vnni ? sco_row_sums(&M->layers[i]) : NULL;
 #pragma omp parallel
     {
         int32_t *ctx = (int32_t *)malloc(sizeof(int32_t) * SCO_ROW_BLOCK * M->window);
@@ -479,7 +590,7 @@ int sco_compress_chunks(const sco_model *M, const int64_t *lut, const uint8_t *t
 #pragma omp for schedule(dynamic, 1)
         for (int64_t c = 0; c < n_chunks; ++c) {
             int64_t nw = 0;
-            int st = sco_compress_one(M, lut, tokens + tok_off[c], lengths[c],
+            int st = sco_compress_one(M, vnni ? wsum : NULL, lut, tokens + tok_off[c], lengths[c],
                                       words + word_off[c], word_cap[c], &nw, ctx, b0, b1, lg);
             word_cnt[c] = (int32_t)nw;
             status[c] = st;
@@ -490,6 +601,7 @@ int sco_compress_chunks(const sco_model *M, const int64_t *lut, const uint8_t *t
         }
         free(ctx); free(b0); free(b1); free(lg);
     }
+    for (int i = 0; i < M->n_layers; ++i) free(wsum[i]);
     return result;
 }
 

@@ -7,12 +7,13 @@ wrong rounding or wrong index fails.
 """
 
 import json
+import os
 from fractions import Fraction
 
 import numpy as np
 import pytest
 
-from conftest import GOLDEN, REFERENCE
+from conftest import GOLDEN, REFERENCE, REPO
 
 
 # ---------------------------------------------------------------- requant / GEMM
@@ -134,6 +135,43 @@ def test_mlp_matches_reference_logits(oracle_mod, oracle_models, name):
     z = np.load(GOLDEN / f"mlp_{name}.npz")
     got = oracle_mod.mlp_forward(oracle_models[name], z["ctx"])
     assert np.array_equal(got, z["logits"])
+
+
+def test_vnni_and_portable_mlp_agree(oracle_mod, tmp_path):
+    """The oracle's AVX-512 VNNI dot products (offset activations, row sums
+    taken off) give the portable C path's logits, bit for bit, on both
+    bundled models and a random per-channel model, with batches that leave
+    partial 4-row groups and blocks."""
+    import subprocess
+    import sys
+    if not oracle_mod.uses_vnni():
+        pytest.skip("host CPU has no AVX-512 VNNI")
+    script = tmp_path / "mlp.py"
+    script.write_text(
+        "import sys, numpy as np\n"
+        f"sys.path[:0] = [{str(REPO)!r}, {str(REPO / 'oracle')!r}]\n"
+        "import oracle\n"
+        "from sigcomp_amd import model_io\n"
+        "ms = [model_io.load_int_model(model_io.DEFAULT_QUANT_LOSSLESS_MODEL_PATH),\n"
+        "      model_io.load_int_model(model_io.DEFAULT_QUANT_LOSSY_MODEL_PATH),\n"
+        "      model_io.random_int_model(seed=9, per_channel=True)]\n"
+        "rng = np.random.default_rng(2)\n"
+        "out = []\n"
+        "for m in ms:\n"
+        "    for rows in (1, 6, 203):\n"
+        "        ctx = rng.integers(0, 257, (rows, 64))\n"
+        "        out.append(oracle.mlp_forward(oracle.OracleModel(m), ctx))\n"
+        "np.savez(sys.argv[1], *out, vnni=oracle.uses_vnni())\n")
+    res = {}
+    for flag in ("0", "1"):
+        f = tmp_path / f"out{flag}.npz"
+        env = dict(os.environ, SCO_NO_VNNI=flag)
+        subprocess.run([sys.executable, str(script), str(f)], check=True, env=env)
+        res[flag] = np.load(f)
+    assert bool(res["0"]["vnni"]) and not bool(res["1"]["vnni"])
+    for k in res["0"].files:
+        if k != "vnni":
+            assert np.array_equal(res["0"][k], res["1"][k]), k
 
 
 def test_mlp_rejects_out_of_range_tokens(oracle_mod, oracle_models):
