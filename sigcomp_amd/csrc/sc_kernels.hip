@@ -826,11 +826,13 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
     const int64_t units = n_chunks / (32 * cu);
     std::vector<int> plan;
     const char *plan_env = getenv("SC_HIP_DEC_PLAN");   // "greedy": largest rt first (comparisons)
-    if (m->dev.pipe == CORE_PIPE_UNI && !(plan_env && std::strcmp(plan_env, "greedy") == 0)) {
+    const char *rt_env = getenv("SC_HIP_DEC_RT");       // n: launches of at most n row tiles (comparisons)
+    const int rt_cap = rt_env ? std::min(std::max(atoi(rt_env), 1), DEC_RT_MAX) : 0;
+    if (m->dev.pipe == CORE_PIPE_UNI && !rt_cap && !(plan_env && std::strcmp(plan_env, "greedy") == 0)) {
         plan = dec_plan(units);
     } else {
-        for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, DEC_RT_MAX))
-            plan.push_back((int)std::min<int64_t>(u, DEC_RT_MAX));
+        const int cap = rt_cap ? rt_cap : DEC_RT_MAX;
+        for (int64_t u = units; u > 0; u -= std::min<int64_t>(u, cap)) plan.push_back((int)std::min<int64_t>(u, cap));
     }
     const int64_t left = n_chunks - units * 32 * cu;
     const int rt_last = plan.empty() ? 0 : plan.back();
