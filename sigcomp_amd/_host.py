@@ -169,8 +169,15 @@ def frame(words: np.ndarray, word_off: np.ndarray, word_cnt: np.ndarray, n_threa
     return out, bounds
 
 
-def parse(payloads, tokens, chunk_len: int, n_threads: int = 0) -> dict:
-    """Parse framed per-read payloads (list of bytes) with their token counts."""
+def parse_word_count(payloads) -> int:
+    """Words parse() writes for these payloads (its words_out size)."""
+    return int(sum(len(p) // 4 for p in payloads))
+
+
+def parse(payloads, tokens, chunk_len: int, n_threads: int = 0, words_out=None) -> dict:
+    """Parse framed per-read payloads (list of bytes) with their token counts.
+    words_out: optional uint32 array of at least parse_word_count(payloads)
+    elements (e.g. pinned memory for the device copy) to hold the words."""
     n = len(payloads)
     tokens = np.asarray(tokens, np.int64).reshape(-1)
     if len(tokens) != n:
@@ -182,7 +189,14 @@ def parse(payloads, tokens, chunk_len: int, n_threads: int = 0) -> dict:
     chunk_begin = _excl_scan(frames)
     n_chunks = int(frames.sum())
     read_word_off = _excl_scan(data_len // 4)
-    words = np.empty(max(int((data_len // 4).sum()), 1), np.uint32)
+    n_words = max(int((data_len // 4).sum()), 1)
+    if words_out is not None:
+        if words_out.dtype != np.uint32 or words_out.ndim != 1 or len(words_out) < n_words \
+                or not words_out.flags.c_contiguous:
+            raise ValueError("words_out must be a contiguous uint32 array of the parse's word count")
+        words = words_out[:n_words]
+    else:
+        words = np.empty(n_words, np.uint32)
     word_off = np.zeros(n_chunks, np.int64)
     word_cnt = np.zeros(n_chunks, np.int32)
     tok_cnt = np.zeros(n_chunks, np.int32)

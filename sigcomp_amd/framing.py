@@ -79,6 +79,14 @@ class ReadFramingMixin:
         reads = [token_array(r) for r in list_of_reads]
         cl = int(self.chunk_len)
         first, sizes = chunk_layout([r.size for r in reads], cl)
+        if hasattr(self, "compress_reads_batches"):
+            # batches of whole reads, each framed while the codec works on later ones
+            out = []
+            for r0, r1, words, word_off, word_cnt in self.compress_reads_batches(reads, batch_size, use_tqdm):
+                buf, bounds = _host.frame(words, word_off, word_cnt)
+                cf = first[r0:r1 + 1] - first[r0]
+                out.extend(buf[bounds[cf[i]]:bounds[cf[i + 1]]].tobytes() for i in range(r1 - r0))
+            return out
         tokens = np.concatenate(reads) if reads else np.zeros(0, np.uint8)
         if hasattr(self, "compress_flat"):
             words, word_off, word_cnt = self.compress_flat(tokens, sizes, batch_size, use_tqdm=use_tqdm)
@@ -99,10 +107,14 @@ class ReadFramingMixin:
             _host.parse(payloads[:bad_len], [int(x) for x in list_of_lengths[:bad_len]], int(self.chunk_len))
             raise ValueError("Token lengths must be nonnegative integers")
         n_tok = np.fromiter((int(x) for x in list_of_lengths), np.int64, count=len(list_of_lengths))
-        pr = _host.parse(payloads, n_tok, int(self.chunk_len))
+        staging = getattr(self, "pinned_words", None)
+        pinned = staging(_host.parse_word_count(payloads)) if staging else None
+        pr = _host.parse(payloads, n_tok, int(self.chunk_len),
+                         words_out=pinned.numpy().view(np.uint32) if pinned is not None else None)
         if hasattr(self, "decompress_flat"):
+            kw = {"words_pinned": pinned} if pinned is not None else {}
             tok, tok_off = self.decompress_flat(pr["words"], pr["word_off"], pr["word_cnt"], pr["tok_cnt"],
-                                                use_tqdm=use_tqdm)
+                                                use_tqdm=use_tqdm, **kw)
         else:
             w = pr["words"]
             encoded = [w[o:o + c].tobytes() for o, c in zip(pr["word_off"], pr["word_cnt"])]

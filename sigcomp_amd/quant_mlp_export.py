@@ -33,6 +33,9 @@ from .model_io import (DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MO
 
 # Chunks staged per kernel launch (bounds host/device staging memory only).
 _MIN_LAUNCH_CHUNKS = 1 << 16
+# Chunks per batch of the pipelined read compression (compress_reads_batches):
+# enough for every compress workgroup to run hundreds of 128-token tiles.
+_MIN_PIPE_CHUNKS = 1 << 13
 
 
 def _progress(it, use_tqdm, desc):
@@ -44,6 +47,16 @@ def _progress(it, use_tqdm, desc):
     except ImportError:
         return it
     return tqdm(it, desc=desc)
+
+
+def _h2d(a, dev):
+    """Host array -> device tensor through pinned memory, without waiting
+    (stream-ordered on the current stream; torch keeps the pinned block
+    until the copy is done)."""
+    a = np.ascontiguousarray(a)
+    pin = torch.empty(a.shape, dtype=torch.from_numpy(a[:0]).dtype, pin_memory=True)
+    pin.numpy()[...] = a
+    return pin.to(dev, non_blocking=True)
 
 
 def _to_device(a, dev):
@@ -210,7 +223,9 @@ class QuantMLPCompression(ReadFramingMixin):
         for s in _progress(range(0, len(lengths), per), use_tqdm, "Compressing chunks (GPU)"):
             ln = lengths[s:s + per]
             nt = int(ln.sum())
-            parts.append(self._compress_batch(tokens[tok0:tok0 + nt], ln))
+            rec = self._compress_enqueue([tokens[tok0:tok0 + nt]], ln)
+            self._compress_gather(rec)
+            parts.append(self._compress_collect(rec))
             tok0 += nt
         if len(parts) == 1:
             return parts[0]
@@ -219,41 +234,107 @@ class QuantMLPCompression(ReadFramingMixin):
         word_off = np.concatenate([p[1] + b for p, b in zip(parts, base)])
         return words, word_off, np.concatenate([p[2] for p in parts])
 
-    def _compress_batch(self, tokens, lengths):
+    def compress_reads_batches(self, reads, max_batch_size=64, use_tqdm=False):
+        """Compress every chunk of `reads` (uint8 token arrays, cut into
+        chunk_len chunks), pipelined over batches of whole reads of at least
+        max(max_batch_size, 8192) chunks: yields (r0, r1, words, word_off,
+        word_cnt) for reads r0 .. r1-1 (dense words of their chunks in order)
+        as soon as they are on the host.  All GPU work is on the current
+        stream; while the caller frames batch k, the GPU compresses batch
+        k + 2 (the word gather and copy of batch k + 1 queue behind it)."""
+        from .framing import chunk_layout
+        cl = int(self.chunk_len)
+        n_tok = np.fromiter((len(r) for r in reads), np.int64, count=len(reads))
+        first, sizes = chunk_layout(n_tok, cl)
+        target = max(int(max_batch_size), _MIN_PIPE_CHUNKS)
+        bounds = [0]
+        while bounds[-1] < len(reads):
+            r0 = bounds[-1]
+            r1 = int(np.searchsorted(first, first[r0] + target, side="left"))
+            bounds.append(min(len(reads), max(r1, r0 + 1)))
+        parts = list(zip(bounds[:-1], bounds[1:]))
+        recs = []
+        for k, (r0, r1) in enumerate(_progress(parts, use_tqdm, "Compressing reads (GPU)")):
+            recs.append(self._compress_enqueue(reads[r0:r1], sizes[first[r0]:first[r1]]))
+            if k >= 1:
+                self._compress_gather(recs[k - 1])
+            if k >= 2:
+                yield (*parts[k - 2], *self._compress_collect(recs[k - 2]))
+                recs[k - 2] = None
+        for k in range(max(0, len(parts) - 2), len(parts)):
+            if k == len(parts) - 1:
+                self._compress_gather(recs[k])
+            yield (*parts[k], *self._compress_collect(recs[k]))
+            recs[k] = None
+
+    def _compress_enqueue(self, pieces, lengths):
+        """Stage the concatenated token arrays `pieces` (chunks of `lengths`)
+        in pinned memory, enqueue the copy and sc_compress_chunks on the
+        current stream, then the copy of the word counts and status back
+        (pinned); returns the batch record."""
+        lengths = np.ascontiguousarray(lengths, np.int32)
         n = len(lengths)
+        n_tokens = int(lengths.sum())
+        dev = self.hip.device
+        pin = torch.empty(max(n_tokens, 1), dtype=torch.uint8, pin_memory=True)
+        if n_tokens:
+            np.concatenate(pieces, out=pin.numpy()[:n_tokens]) if len(pieces) > 1 else \
+                np.copyto(pin.numpy()[:n_tokens], pieces[0])
         tok_off = np.zeros(n, dtype=np.int64)
         np.cumsum(lengths[:-1], out=tok_off[1:])
-        n_tokens = int(lengths.sum())
-        if n_tokens == 0:
-            tokens = np.zeros(1, np.uint8)
         cap = lengths + 2
         word_off = np.zeros(n, dtype=np.int64)
         np.cumsum(cap[:-1], dtype=np.int64, out=word_off[1:])
-        dev = self.hip.device
-        d = lambda a: _to_device(a, dev)
-        t_tokens, t_tok_off, t_len = d(tokens), d(tok_off), d(lengths)
-        t_word_off, t_cap = d(word_off), d(cap.astype(np.int32))
-        words, cnt, status, ws = self._compress_buffers(n, n_tokens, int(cap.sum()))
-        L = _hip.lib()
+        rec = {"n": n, "dev": dev}
         with torch.cuda.device(dev):
-            _hip.check(L.sc_compress_chunks(
+            t_tokens = pin.to(dev, non_blocking=True)
+            d = lambda a: _h2d(a, dev)
+            t_tok_off, t_len, t_word_off, t_cap = d(tok_off), d(lengths), d(word_off), d(cap.astype(np.int32))
+            words, cnt, status, ws = self._compress_buffers(n, n_tokens, int(cap.sum()))
+            _hip.check(_hip.lib().sc_compress_chunks(
                 self.hip.handle, _hip.ptr(t_tokens), _hip.ptr(t_tok_off), _hip.ptr(t_len), n,
                 n_tokens, _hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(t_cap), _hip.ptr(cnt),
                 _hip.ptr(status), _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
-            st = status.cpu().numpy()
-            if st.any():
-                b = int(np.flatnonzero(st)[0])
-                raise OverflowError(f"range-coder output capacity exceeded in stream {b}")
-            # pack the used words densely on the device, then one transfer
-            cnt_np = cnt.cpu().numpy()
-            dense_off = np.zeros(n, dtype=np.int64)
-            np.cumsum(cnt_np[:-1], dtype=np.int64, out=dense_off[1:])
-            dense = torch.empty(max(int(cnt_np.sum()), 1), dtype=torch.int32, device=dev)
-            t_dense_off = d(dense_off)
-            _hip.check(L.sc_gather_words(_hip.ptr(words), _hip.ptr(t_word_off), _hip.ptr(cnt), n,
-                                         _hip.ptr(dense), _hip.ptr(t_dense_off), _hip.stream_ptr()))
-            words_np = dense.cpu().numpy().view(np.uint32)
-        return words_np, dense_off, cnt_np
+            h_cnt = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            h_status = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            h_cnt.copy_(cnt, non_blocking=True)
+            h_status.copy_(status, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+        rec.update(keep=(pin, t_tokens, t_tok_off, t_len, t_cap, ws), words=words, cnt=cnt, t_word_off=t_word_off,
+                   h_cnt=h_cnt, h_status=h_status, ev_cnt=ev)
+        return rec
+
+    def _compress_gather(self, rec):
+        """Wait for a batch's word counts, then enqueue the dense word
+        gather and its copy into pinned memory."""
+        rec["ev_cnt"].synchronize()
+        st = rec["h_status"].numpy()
+        if st.any():
+            b = int(np.flatnonzero(st)[0])
+            raise OverflowError(f"range-coder output capacity exceeded in stream {b}")
+        n, dev = rec["n"], rec["dev"]
+        cnt_np = rec["h_cnt"].numpy().copy()
+        dense_off = np.zeros(n, dtype=np.int64)
+        np.cumsum(cnt_np[:-1], dtype=np.int64, out=dense_off[1:])
+        total = max(int(cnt_np.sum()), 1)
+        with torch.cuda.device(dev):
+            dense = torch.empty(total, dtype=torch.int32, device=dev)
+            t_dense_off = _h2d(dense_off, dev)
+            _hip.check(_hip.lib().sc_gather_words(_hip.ptr(rec["words"]), _hip.ptr(rec["t_word_off"]),
+                                                  _hip.ptr(rec["cnt"]), n, _hip.ptr(dense), _hip.ptr(t_dense_off),
+                                                  _hip.stream_ptr()))
+            h_words = torch.empty(total, dtype=torch.int32, pin_memory=True)
+            h_words.copy_(dense, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+        rec.update(keep2=(dense, t_dense_off), h_words=h_words, ev_words=ev, dense_off=dense_off, cnt_np=cnt_np)
+
+    @staticmethod
+    def _compress_collect(rec):
+        """A gathered batch's (dense words, offsets, counts) on the host."""
+        rec["ev_words"].synchronize()
+        return rec["h_words"].numpy().view(np.uint32), rec["dense_off"], rec["cnt_np"]
 
     def _compress_buffers(self, n, n_tokens, n_words):
         dev = self.hip.device
@@ -265,6 +346,12 @@ class QuantMLPCompression(ReadFramingMixin):
         return words, cnt, status, ws
 
     # ---------------------------------------------------------- decompress
+
+    @staticmethod
+    def pinned_words(n_words):
+        """A pinned int32 host tensor for n_words range-coder words (parse
+        target, copied to the device without staging)."""
+        return torch.empty(max(int(n_words), 1), dtype=torch.int32, pin_memory=True)
 
     def _decompress_workspace(self, n):
         """Per-call decode state (sc_decompress_workspace_bytes): a tensor
@@ -303,7 +390,7 @@ class QuantMLPCompression(ReadFramingMixin):
         tok, tok_off = self.decompress_flat(flat, word_off, cnt, lengths)
         return [tok[tok_off[i]:tok_off[i] + lengths[i]].copy() for i in range(n)]
 
-    def decompress_flat(self, words, word_off, word_cnt, lengths, use_tqdm=False):
+    def decompress_flat(self, words, word_off, word_cnt, lengths, use_tqdm=False, words_pinned=None):
         """Decompress chunks given as one uint32 word array with per-chunk
         word offsets / counts and token lengths -> (uint8 tokens of all
         chunks concatenated in chunk order, per-chunk token offsets).  One
@@ -333,20 +420,30 @@ class QuantMLPCompression(ReadFramingMixin):
         # length and stops at its own longest one
         order = np.argsort(-lengths, kind="stable")
         dev = self.hip.device
-        d = lambda a: _to_device(a, dev)
-        t_words = d(words.view(np.int32))
-        t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(lengths[order]), d(tok_off[order])
-        tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)
-        status = torch.empty(n, dtype=torch.int32, device=dev)
         len_host = np.ascontiguousarray(lengths[order])
         with torch.cuda.device(dev):
+            # every copy through pinned memory, stream-ordered: the call
+            # waits once, for the tokens
+            if words_pinned is not None and words_pinned.data_ptr() == words.ctypes.data:
+                t_words = words_pinned.to(dev, non_blocking=True)
+            else:
+                t_words = _h2d(words.view(np.int32), dev)
+            d = lambda a: _h2d(a, dev)
+            t_woff, t_cnt, t_len, t_toff = d(word_off[order]), d(cnt[order]), d(len_host), d(tok_off[order])
+            tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, device=dev)
+            status = torch.empty(n, dtype=torch.int32, device=dev)
             ws = self._decompress_workspace(n)
             _hip.check(_hip.lib().sc_decompress_chunks(
                 self.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt),
                 _hip.ptr(t_len), n, _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status),
                 len_host.ctypes.data, _hip.ptr(ws), ws.numel(), _hip.stream_ptr()))
-        st = status.cpu().numpy()
+            h_tokens = torch.empty(max(n_tokens, 1), dtype=torch.uint8, pin_memory=True)
+            h_status = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            h_tokens.copy_(tokens, non_blocking=True)
+            h_status.copy_(status, non_blocking=True)
+            torch.cuda.current_stream().synchronize()
+        st = h_status.numpy()
         if st.any():
             raise ValueError("invalid range stream or mismatching entropy model in chunk "
                              f"{int(order[np.flatnonzero(st)[0]])}")
-        return tokens.cpu().numpy()[:n_tokens], tok_off
+        return h_tokens.numpy()[:n_tokens], tok_off

@@ -690,3 +690,26 @@ def test_mfma_burn_hook_computes_its_products():
     v = np.arange(16)[None, :]
     exp = D[8 * (v // 4) + 4 * (lane // 32) + v % 4, lane % 32].astype(np.int32)
     assert all(np.array_equal(got[g, w], exp) for g in range(groups) for w in range(4))
+
+
+def test_pipelined_read_compression_matches_single_batch(codecs, oracle_mod, oracle_models, monkeypatch):
+    """batch_inference_reads compresses reads in pipelined batches of whole
+    reads (compress_reads_batches): with batches of ~8 chunks (many batches,
+    reads of 0..9 chunks, empty reads at a batch edge) every payload equals
+    the single-batch run's and the oracle's framing of its chunks, and the
+    payloads decode back."""
+    from framing_ref import chunk_views, frame
+    from sigcomp_amd import quant_mlp_export
+    rng = np.random.default_rng(21)
+    lens = rng.integers(0, 9 * 2048, 40)
+    lens[[3, 4, 17]] = 0
+    reads = [rng.integers(0, 70, n).astype(np.uint8) for n in lens]
+    codec = codecs["lossless"]
+    one = codec.batch_inference_reads(list_of_reads=reads, batch_size=20480)
+    monkeypatch.setattr(quant_mlp_export, "_MIN_PIPE_CHUNKS", 8)
+    many = codec.batch_inference_reads(list_of_reads=reads, batch_size=1)
+    assert many == one
+    for r in (0, 3, 5, 39):
+        assert many[r] == frame(oracle_mod.compress_chunks(oracle_models["lossless"], chunk_views(reads[r], 2048)))
+    back = codec.batch_inference_reads(list_of_compressed_reads=many, list_of_lengths=[int(n) for n in lens])
+    assert all(np.array_equal(a, b) for a, b in zip(reads, back))
