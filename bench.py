@@ -286,7 +286,12 @@ def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
         "roofline_compress": roofline("k_compress_mlp", n_tokens, t_c, name, "coded"),
     }
     if e2e:
+        # the first pass also allocates the pinned staging buffers (torch keeps
+        # them cached): report the second, as a process that compresses
+        # batch after batch runs
+        first = end_to_end(codec, reads, cfg["lsb"])
         res["end_to_end"] = end_to_end(codec, reads, cfg["lsb"])
+        res["end_to_end"]["first_pass_msamples_s"] = first["msamples_s_round_trip"]
     return res, dict(model=codec.model, chunks=chunks, samples=samples, words=words_np, word_off=word_off,
                      word_cnt=cnt_np)
 
@@ -748,7 +753,7 @@ def run_one(args):
     sampler = PowerSampler()
     try:
         res, raw = run_codec(args.config, args.steps, args.warmup, sampler, n_reads=args.n_reads,
-                             e2e=args.config == "c3", copy_mib=args.copy_mib)
+                             e2e=args.config == "c3" and not args.no_end_to_end, copy_mib=args.copy_mib)
     finally:
         sampler.stop()
     out = headline(res, args.steps, args.warmup)
@@ -772,6 +777,8 @@ def main():
     ap.add_argument("--n-reads", type=int, default=None)
     ap.add_argument("--rows", type=int, default=1 << 20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-end-to-end", action="store_true",
+                    help="single configurations: skip the PCIe-inclusive read pipeline pass (profiling runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="run one elementwise copy of this many MiB first (PMC calibration)")
     args = ap.parse_args()
