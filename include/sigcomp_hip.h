@@ -26,10 +26,15 @@
  *    lives in memory the caller passes (workspace, state and output arrays);
  *    calls that share such memory must not overlap.
  *
- * Architecture supported by the kernels: window 64, embedding 257 x 128,
- * layer 0 8192 -> 512, n_layers - 2 hidden layers 512 -> 512, last layer
- * 512 -> 256 (the bundled lossless and lossy checkpoints,
- * quant_mlp_export.py:211-213, cpu_int_inference.py:395-445).
+ * Architectures: any window W, embedding 257 x E and chain of n_layers
+ * (1..16) linear layers from W * E inputs to 256 logits, as the reference's
+ * GPU codec takes (quant_mlp_export.py:21-101,215-269).  The bundled one
+ * (window 64, embedding 257 x 128, layer 0 8192 -> 512, n_layers - 2 hidden
+ * layers 512 -> 512, last layer 512 -> 256: both bundled checkpoints,
+ * quant_mlp_export.py:211-213, cpu_int_inference.py:395-445) runs the
+ * specialised persistent kernels; any other runs the generic path (one
+ * launch per stage, scratch memory from hipMallocAsync on the call's
+ * stream), with identical results for any model.
  */
 #ifndef SIGCOMP_HIP_H
 #define SIGCOMP_HIP_H
@@ -92,9 +97,10 @@ const uint64_t *sc_model_lut(const sc_model *model);
  * shift per layer, as in both bundled checkpoints;
  * tiles of up to 128 rows; every kernel), 1 = pipelined core with
  * per-channel constants (the explicit-context kernels; compress and
- * decompress run the plain core), 0 = plain core (any valid model; also
- * selected by SC_HIP_PLAIN_CORE=1 in the environment at sc_model_create).
- * All give identical results.  No reference counterpart (diagnostic). */
+ * decompress run the plain core), 0 = plain core (any model of the bundled
+ * architecture; also selected by SC_HIP_PLAIN_CORE=1 in the environment at
+ * sc_model_create), 3 = generic path (any other architecture).  All give
+ * identical results.  No reference counterpart (diagnostic). */
 int sc_model_core(const sc_model *model);
 
 /* MLP forward on explicit context windows: ctx int64 [rows, 64] (device,
@@ -240,7 +246,8 @@ int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int
  * SC_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (on different streams or threads) race.  With
  * lengths_host NULL the call waits for its stream, as sc_decompress_chunks
- * does. */
+ * does.  Models of the bundled architecture only (SC_ERR_UNSUPPORTED for a
+ * generic model, whose path allocates scratch memory). */
 #define SC_STATIC_DEC_MAX_CHUNKS 65536
 int sc_decompress_chunks_static(const sc_model *model, const uint32_t *words, const int64_t *word_off,
                                 const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,

@@ -24,7 +24,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libsigcomp_hip.so"
 # Translation units of libsigcomp_hip.so as (source, defines): the large MLP
 # kernels are split over several units so that they compile in parallel.
-UNITS = [(CSRC / "sc_kernels.hip", ()), (CSRC / "sc_comp.hip", ()),
+UNITS = [(CSRC / "sc_kernels.hip", ()), (CSRC / "sc_comp.hip", ()), (CSRC / "sc_gen.hip", ()),
          (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=0",)), (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=1",)),
          *[(CSRC / "sc_dec.hip", (f"SC_DEC_RT={rt}",)) for rt in range(1, 6)]]
 SOURCES = sorted({src for src, _ in UNITS})
@@ -32,7 +32,8 @@ HOST_LIB = PKG / "libsigcomp_host.so"
 HOST_SOURCES = [CSRC / "sc_host.cpp"]
 HOST_FLAGS = ["-O3", "-march=x86-64-v3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra",
               f"-I{REPO / 'include'}"]
-HEADERS = [CSRC / "sc_device.h", CSRC / "sc_pipe.h", CSRC / "sc_kernels.h", REPO / "include" / "sigcomp_hip.h"]
+HEADERS = [CSRC / "sc_device.h", CSRC / "sc_pipe.h", CSRC / "sc_kernels.h", CSRC / "sc_gen.h",
+           REPO / "include" / "sigcomp_hip.h"]
 ARCH = os.environ.get("SIGCOMP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

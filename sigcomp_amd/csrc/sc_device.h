@@ -62,7 +62,8 @@ struct ModelDev {
     const int8_t *emb;       // [257][128] row-major
     const uint64_t *lut;     // [256]
     int32_t n_layers;
-    int32_t pipe;            // MLP core: CORE_PLAIN, CORE_PIPE or CORE_PIPE_UNI (sc_model_create)
+    int32_t pipe;            // MLP core: CORE_PLAIN, CORE_PIPE, CORE_PIPE_UNI or CORE_GENERIC (sc_model_create)
+    int32_t window, emb_dim; // context tokens per row and embedding width (64 and 128 but for CORE_GENERIC)
 };
 
 // MLP cores.  CORE_PIPE (sc_pipe.h) needs every layer fast with ReLU on all
@@ -71,6 +72,9 @@ struct ModelDev {
 // rq_words_uni, and the LDS parameter slots hold only biases).  All three
 // give identical results.
 constexpr int CORE_PLAIN = 0, CORE_PIPE = 1, CORE_PIPE_UNI = 2;
+// CORE_GENERIC: any other architecture (window, embedding width, layer
+// widths and count), one launch per stage (sc_gen.hip).
+constexpr int CORE_GENERIC = 3;
 
 // ---------------------------------------------------------------- LDS layouts
 

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../include/sigcomp_hip.h"
+#include "sc_gen.h"
 #include "sc_kernels.h"
 
 using namespace sc;
@@ -424,6 +425,23 @@ std::vector<int8_t> pack_weight(const int8_t *w, int n, int k, bool perm_k) {
     return out;
 }
 
+// Generic path: W [n, k] into fragments of ceil(n/32) x ceil(k/32) tiles,
+// zero beyond n and k, natural column order (fragment (nt, kt), lane l,
+// byte b: row nt*32 + l%32, column kt*32 + (l/32)*16 + b).
+std::vector<int8_t> pack_weight_padded(const int8_t *w, int n, int k) {
+    const int NT = (n + 31) / 32, KT = (k + 31) / 32;
+    std::vector<int8_t> out((size_t)NT * KT * 1024, 0);
+    for (int nt = 0; nt < NT; ++nt)
+        for (int kt = 0; kt < KT; ++kt)
+            for (int l = 0; l < 64; ++l)
+                for (int b = 0; b < 16; ++b) {
+                    const int row = nt * 32 + (l & 31), col = kt * 32 + (l >> 5) * 16 + b;
+                    if (row < n && col < k)
+                        out[(((size_t)nt * KT + kt) * 64 + l) * 16 + b] = w[(size_t)row * k + col];
+                }
+    return out;
+}
+
 hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
 // Per-step cost of a full-wave decode launch at rt = 1 .. DEC_RT_MAX row
@@ -509,16 +527,21 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
                     int32_t device, sc_model **out) {
     if (!out || !emb || !layers || !exp_lut) return fail(SC_ERR_ARG, "null argument");
     *out = nullptr;
-    if (emb_rows != EMB_ROWS || emb_dim != EDIM || window != WIN)
-        return fail(SC_ERR_UNSUPPORTED, "kernels support window 64 and a 257 x 128 embedding");
-    if (n_layers < 2 || n_layers > MAX_LAYERS)
-        return fail(SC_ERR_UNSUPPORTED, "kernels support 2..16 linear layers");
+    // any architecture whose layers chain from window * emb_dim inputs to 256
+    // logits; the bundled one (window 64, 257 x 128 embedding, 8192 -> 512,
+    // 512 -> 512 ..., 512 -> 256) runs the specialised kernels, any other
+    // the generic path (CORE_GENERIC)
+    if (emb_rows != EMB_ROWS) return fail(SC_ERR_UNSUPPORTED, "the embedding needs 257 rows (256 symbols and SOS)");
+    if (window < 1 || emb_dim < 1 || (int64_t)window * emb_dim > (int64_t(1) << 20))
+        return fail(SC_ERR_UNSUPPORTED, "window and embedding width must be positive, product at most 2**20");
+    if (n_layers < 1 || n_layers > MAX_LAYERS) return fail(SC_ERR_UNSUPPORTED, "kernels support 1..16 linear layers");
+    bool special = emb_dim == EDIM && window == WIN && n_layers >= 2;
     for (int i = 0; i < n_layers; ++i) {
         const sc_layer_desc &L = layers[i];
-        const int want_k = i == 0 ? K0 : HID;
-        const int want_n = i == n_layers - 1 ? VOCAB : HID;
-        if (L.k != want_k || L.n != want_n)
-            return fail(SC_ERR_UNSUPPORTED, "kernels support 8192->512, 512->512 ..., 512->256 layers");
+        const int64_t want_k = i == 0 ? (int64_t)window * emb_dim : layers[i - 1].n;
+        if (L.k != want_k || L.n < 1 || L.n > (1 << 16) || (i == n_layers - 1 && L.n != VOCAB))
+            return fail(SC_ERR_UNSUPPORTED, "layers must chain from window * emb_dim inputs to 256 logits");
+        special = special && L.k == (i == 0 ? K0 : HID) && L.n == (i == n_layers - 1 ? VOCAB : HID);
         if (!L.weight || !L.bias || !L.m0 || !L.shift) return fail(SC_ERR_ARG, "null layer array");
         for (int j = 0; j < L.n; ++j) {
             if (L.m0[j] < 0 || L.m0[j] > (int64_t(1) << 31))
@@ -549,9 +572,11 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     m->n_cu = prop.multiProcessorCount;
     int rc = SC_OK;
     {
-        std::vector<int8_t> e(emb, emb + EMB_ROWS * EDIM);
+        std::vector<int8_t> e(emb, emb + (size_t)EMB_ROWS * emb_dim);
         rc = upload(m, e, &m->dev.emb);
     }
+    m->dev.window = window;
+    m->dev.emb_dim = emb_dim;
     if (rc == SC_OK) {
         std::vector<uint64_t> lut(exp_lut, exp_lut + VOCAB);
         rc = upload(m, lut, &m->dev.lut);
@@ -559,7 +584,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
     for (int i = 0; i < n_layers && rc == SC_OK; ++i) {
         const sc_layer_desc &L = layers[i];
         LayerDev &D = m->dev.layer[i];
-        std::vector<int8_t> packed = pack_weight(L.weight, L.n, L.k, i > 0);
+        std::vector<int8_t> packed = special ? pack_weight(L.weight, L.n, L.k, i > 0) : pack_weight_padded(L.weight, L.n, L.k);
         const int8_t *wdev = nullptr;
         rc = upload(m, packed, &wdev);
         D.w = (const v4i *)wdev;
@@ -583,6 +608,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
             sh[j] = (uint8_t)sj;
             fast = fast && mj < (int64_t(1) << 31) && sj >= 32;
         }
+        fast = fast && special;   // the generic path requantises with the full 64-bit form
         if (fast)
             for (int j = 0; j < L.n; ++j) sh[j] = (uint8_t)(sh[j] - 32);
         D.fast = fast ? 1 : 0;
@@ -594,10 +620,12 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         D.ush = uni ? sh[0] : 0;
         D.uhi = uni ? (int32_t)std::min<int64_t>((int64_t(128) << sh[0]) - 1, INT32_MAX) : 0;
         D.ulo = uni ? (int32_t)std::max<int64_t>(-(int64_t(128) << sh[0]), INT32_MIN) : 0;
-        std::vector<uint32_t> par((size_t)(L.n / 32) * PAR_DWORDS, 0u);
-        for (int nt = 0; nt < L.n / 32; ++nt) {
+        // (padded n-tiles of the generic path: bias, m0 and shift 0)
+        const int n_tiles = (L.n + 31) / 32;
+        std::vector<uint32_t> par((size_t)n_tiles * PAR_DWORDS, 0u);
+        for (int nt = 0; nt < n_tiles; ++nt) {
             uint32_t *blk = par.data() + (size_t)nt * PAR_DWORDS;
-            for (int x = 0; x < 32; ++x) {
+            for (int x = 0; x < 32 && nt * 32 + x < L.n; ++x) {
                 const int j = nt * 32 + x;
                 blk[x] = (uint32_t)L.bias[j];
                 blk[32 + x] = m0[j];
@@ -607,7 +635,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         rc = upload(m, par, &D.par);
         if (rc) break;
         D.n = L.n;
-        D.kt = L.k / 32;
+        D.kt = (L.k + 31) / 32;
         D.relu = L.relu ? 1 : 0;
         D.bytes = (int32_t)packed.size();
     }
@@ -619,7 +647,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         if (!m->dev.layer[i].fast || m->dev.layer[i].relu != (i < n_layers - 1 ? 1 : 0)) pipe = false;
         if (!m->dev.layer[i].uni) uni = false;
     }
-    m->dev.pipe = !pipe ? CORE_PLAIN : uni ? CORE_PIPE_UNI : CORE_PIPE;
+    m->dev.pipe = !special ? CORE_GENERIC : !pipe ? CORE_PLAIN : uni ? CORE_PIPE_UNI : CORE_PIPE;
     if (rc != SC_OK) {
         sc_model_destroy(m);
         return rc;
@@ -647,6 +675,12 @@ static int mlp_context_launch(const sc_model *m, const int64_t *ctx, int64_t row
     if (!ctx || (mode == OUT_LOGITS && !logits) || (mode == OUT_CDF32 && !cdf))
         return fail(SC_ERR_ARG, "null device pointer");
     DeviceGuard guard(m->device);
+    if (m->dev.pipe == CORE_GENERIC) {
+        std::string err;
+        const int rc = gen_mlp_forward(m->dev, ctx, rows, mode == OUT_LOGITS ? logits : nullptr,
+                                       mode == OUT_CDF32 ? cdf : nullptr, status, as_stream(stream), err);
+        return rc ? fail(rc, err) : SC_OK;
+    }
     const int64_t tiles = (rows + R_TILE - 1) / R_TILE;
     const int grid = (int)std::min<int64_t>(tiles, m->n_cu);
     if (mode == OUT_LOGITS) launch_mlp_context<OUT_LOGITS>(m->dev, grid, as_stream(stream), ctx, rows, logits, cdf, status);
@@ -751,11 +785,17 @@ int sc_compress_chunks(const sc_model *m, const uint8_t *tokens, const int64_t *
                        n_chunks, tile_start, desc, max_tiles);
     rc = check_launch("k_tile_table");
     if (rc) return rc;
-    // one workgroup per CU (or per tile when there are fewer tiles)
-    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(max_tiles, m->n_cu));
-    launch_compress_mlp(m->dev, grid, s, tokens, n_chunks, tile_start, desc, max_tiles, pairs);
-    rc = check_launch("k_compress_mlp");
-    if (rc) return rc;
+    if (m->dev.pipe == CORE_GENERIC) {
+        std::string err;
+        rc = gen_compress(m->dev, tokens, tile_start, n_chunks, desc, max_tiles, pairs, s, err);
+        if (rc) return fail(rc, err);
+    } else {
+        // one workgroup per CU (or per tile when there are fewer tiles)
+        const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(max_tiles, m->n_cu));
+        launch_compress_mlp(m->dev, grid, s, tokens, n_chunks, tile_start, desc, max_tiles, pairs);
+        rc = check_launch("k_compress_mlp");
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL(k_encode_pairs, dim3((unsigned)((n_chunks + 255) / 256)), dim3(256), 0, s, pairs, tok_off,
                        lengths, n_chunks, words, word_off, word_cap, word_cnt, status);
     return check_launch("k_encode_pairs");
@@ -810,6 +850,24 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
                           const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
                           int32_t *status, const int32_t *lengths_host, DecState *state, int32_t *stat_dev,
                           hipStream_t s) {
+    if (m->dev.pipe == CORE_GENERIC) {
+        // step by step over all chunks: the longest chunk bounds the steps
+        int32_t st4[4];
+        if (lengths_host) {
+            host_len_stats(lengths_host, n_chunks, 0, 0, 0, st4);
+        } else {
+            hipLaunchKernelGGL(k_dec_lengths, dim3(1), dim3(1024), 0, s, lengths, n_chunks, (int64_t)0, (int64_t)0,
+                               (int64_t)0, stat_dev);
+            int rc = check_launch("k_dec_lengths");
+            if (rc) return rc;
+            SC_HIP(hipMemcpyAsync(st4, stat_dev, sizeof(st4), hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+            SC_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+        }
+        std::string err;
+        const int rc = gen_decompress(m->dev, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status,
+                                      state, st4[0], s, err);
+        return rc ? fail(rc, err) : SC_OK;
+    }
     // Launch plan.  A workgroup owns 32*rt consecutive chunks for the whole
     // decode, one workgroup per CU, and every launch but the last is one
     // full wave of n_cu workgroups.  The chunks of the full waves make
@@ -942,6 +1000,9 @@ int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const 
     if (n_chunks == 0) return SC_OK;
     if (!words || !word_off || !word_cnt || !lengths || !tokens || !tok_off || !status)
         return fail(SC_ERR_ARG, "null device pointer");
+    if (m->dev.pipe == CORE_GENERIC)
+        return fail(SC_ERR_UNSUPPORTED, "sc_decompress_chunks_static runs the bundled architecture's kernels only "
+                                        "(the generic path allocates scratch memory)");
     DeviceGuard guard(m->device);
     int rc = SC_OK;
     void *base = scratch_ptr(m->device, &rc);

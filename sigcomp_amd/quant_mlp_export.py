@@ -95,9 +95,10 @@ class HipModel:
         self.exp_lut = torch.from_numpy(lut.copy()).to(self.device)
         # MLP core of the kernels (sc_model_core): 2 = pipelined with per-tensor
         # requant constants (every kernel), 1 = pipelined for the explicit-context
-        # kernels only, 0 = plain
+        # kernels only, 0 = plain, 3 = generic (an architecture other than the
+        # bundled one)
         self.core = int(_hip.lib().sc_model_core(handle))
-        self.pipelined = self.core != 0
+        self.pipelined = self.core in (1, 2)
 
     def __del__(self):
         h = getattr(self, "handle", None)
