@@ -55,6 +55,9 @@ extern "C" {
 #define SC_STATUS_CAPACITY 1        /* encoder output capacity exceeded (OverflowError) */
 #define SC_STATUS_INVALID_STREAM 2  /* decoder: scale == 0 or quantile >= 2**24 (ValueError) */
 #define SC_STATUS_BAD_TOKEN 3       /* context token outside [0, 256] (ValueError) */
+#define SC_STATUS_SYNC_TIMEOUT 4    /* decoder: the workgroups sharing a small decode's layer 0
+                                       waited too long for each other (RuntimeError; tokens
+                                       unspecified) */
 
 #define SC_VOCAB 256
 #define SC_SOS 256
@@ -207,8 +210,10 @@ int sc_gather_words(const uint32_t *words, const int64_t *word_off, const int32_
 int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t *out, void *stream);
 
 /* Bytes of device workspace sc_decompress_chunks needs for n_chunks chunks:
- * the coder state of every chunk between step segments (40 bytes per chunk)
- * and the launch plan's four length statistics, each 256-byte aligned. */
+ * the coder state of every chunk between step segments (40 bytes per chunk),
+ * the launch plan's four length statistics, and the exchange buffers of a
+ * split decode (32 KiB per 32 chunks, at most 64 such groups, and 16 bytes of
+ * step flags per group), each part 256-byte aligned. */
 int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
 
 /* Decompress n_chunks chunks with persistent kernels: every workgroup owns a
@@ -228,8 +233,12 @@ int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
  * descending length (as QuantMLPCompression passes them) give the shortest
  * schedule: the shortest chunks are then left over after the full waves of
  * workgroups and follow the shortest chunks of the last full wave in the
- * same rows.  Replaces QuantMLPCompression.decompress_chunks /
- * _decompress_chunks_gpu (quant_mlp_export.py:325-377); output equals
+ * same rows.  A launch of few 32-chunk groups (at most a quarter of the
+ * CUs) runs split: four workgroups per group share layer 0 and wait for
+ * each other every step (a cooperative launch, so all are resident; a
+ * bounded wait, SC_STATUS_SYNC_TIMEOUT when it expires).  Replaces
+ * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
+ * (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */
 int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int64_t *word_off,
                          const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,
@@ -241,7 +250,8 @@ int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  sc_decompress_chunks with its workspace replaced by a
  * static device array the library holds on each GPU it runs on until the
- * process ends (SC_STATIC_DEC_MAX_CHUNKS chunks of coder state, 2.5 MiB);
+ * process ends (SC_STATIC_DEC_MAX_CHUNKS chunks of coder state and the
+ * split decode's exchange buffers, 4.6 MiB);
  * the call allocates nothing.  n_chunks above SC_STATIC_DEC_MAX_CHUNKS ->
  * SC_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (on different streams or threads) race.  With

@@ -20,6 +20,7 @@ SC_STATUS_OK = 0
 SC_STATUS_CAPACITY = 1
 SC_STATUS_INVALID_STREAM = 2
 SC_STATUS_BAD_TOKEN = 3
+SC_STATUS_SYNC_TIMEOUT = 4
 
 EXPORTED = (
     "sc_last_error", "sc_version", "sc_model_create", "sc_model_destroy", "sc_model_lut",

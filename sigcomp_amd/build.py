@@ -25,6 +25,7 @@ LIB = PKG / "libsigcomp_hip.so"
 # Translation units of libsigcomp_hip.so as (source, defines): the large MLP
 # kernels are split over several units so that they compile in parallel.
 UNITS = [(CSRC / "sc_kernels.hip", ()), (CSRC / "sc_comp.hip", ()), (CSRC / "sc_gen.hip", ()),
+         (CSRC / "sc_dec_split.hip", ()),
          (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=0",)), (CSRC / "sc_ctx.hip", ("SC_CTX_MODE=1",)),
          *[(CSRC / "sc_dec.hip", (f"SC_DEC_RT={rt}",)) for rt in range(1, 6)]]
 SOURCES = sorted({src for src, _ in UNITS})

@@ -18,7 +18,7 @@ void launch_decompress<SC_DEC_RT>(const ModelDev &M, unsigned grid, hipStream_t 
     auto *kern = M.pipe == CORE_PIPE_UNI && RT <= 4 ? k_decompress<RT, (RT <= 4 ? CORE_PIPE_UNI : CORE_PLAIN)>
                                                     : k_decompress<RT, CORE_PLAIN>;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), 0, s, M, words, woff, wcnt, len, count, tokens, toff, st,
-                       state, t_begin, t_end, n_second);
+                       state, t_begin, t_end, n_second, (uint8_t *)nullptr, 0);
 }
 
 }  // namespace sc

@@ -1,8 +1,9 @@
 // sc_kernels.h -- the MLP kernel templates of libsigcomp_hip (explicit
 // context windows, teacher-forced compress, persistent decompress) and the
 // host launchers that instantiate them.  Each launcher is defined in a
-// translation unit of its own (sc_ctx.hip, sc_comp.hip, sc_dec.hip), so the
-// large kernels compile in parallel; sc_kernels.hip holds the C ABI.
+// translation unit of its own (sc_ctx.hip, sc_comp.hip, sc_dec.hip,
+// sc_dec_split.hip), so the large kernels compile in parallel;
+// sc_kernels.hip holds the C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,6 +27,19 @@ struct DecState {
     int32_t rpos, stat, cur, start;
 };
 
+// Split decode (small batches): SPLIT_P workgroups per 32-chunk group share
+// layer 0 (see k_decompress).  Per group the exchange workspace holds two
+// parity buffers of 32 rows x 512 feature bytes; after the buffers of all
+// groups come SPLIT_P int32 step flags per group.
+constexpr int SPLIT_P = 4;
+constexpr int XCH_ROW = HID;                 // bytes per row of an exchange buffer
+constexpr int XCH_PAR = 32 * XCH_ROW;        // one parity buffer
+constexpr int XCH_GROUP = 2 * XCH_PAR;       // both parities of one group
+constexpr int XCH_MAX_GROUPS = 64;           // 64 x 4 workgroups fill the 256 CUs
+constexpr int64_t xch_bytes(int64_t groups) {
+    return groups * XCH_GROUP + (groups * SPLIT_P * 4 + 255) / 256 * 256;
+}
+
 // Host launchers (stream-ordered, no error check: the caller checks
 // hipGetLastError).  The MLP core follows M.pipe.
 template <int MODE>
@@ -37,6 +51,16 @@ template <int RT>
 void launch_decompress(const ModelDev &M, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                        const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
                        int32_t *st, DecState *state, int32_t t_begin, int32_t t_end, int64_t n_second);
+// The split decode of `groups` 32-chunk groups (pipelined per-tensor core
+// only): a cooperative launch of groups * SPLIT_P workgroups, so that all
+// are resident at once; returns the launch's error (the caller falls back
+// when the device cannot hold them).  `xch` = xch_bytes(groups) bytes, the
+// flags zeroed before the first step segment of a call; each wait for the
+// peers gives up after spin_max polls (SYNC_SPIN_MAX).
+hipError_t launch_decompress_split(const ModelDev &M, unsigned groups, hipStream_t s, const uint32_t *words,
+                                   const int64_t *woff, const int32_t *wcnt, const int32_t *len, int64_t count,
+                                   uint8_t *tokens, const int64_t *toff, int32_t *st, DecState *state,
+                                   int32_t t_begin, int32_t t_end, uint8_t *xch, int32_t spin_max);
 
 namespace {
 
@@ -251,7 +275,147 @@ __device__ __forceinline__ uint64_t dec_init_point(const uint32_t *w, int cnt, i
     return point;
 }
 
-template <int RT, int CORE>
+// ---- split decode: layer 0 shared by the P workgroups of a row group -----
+//
+// With few chunks a decode has few 32-row workgroups, and each step streams
+// the whole model (6.2 MB) through one CU's vector L1 for 32 rows.  In the
+// split decode the P workgroups of a group each compute 512 / P of layer
+// 0's features (n-tile 16 / P * slice + wave: one n-tile per wave at
+// P = 4), exchange them through memory, and then all of them run the
+// hidden layers, the output layer and the decoder step on the same data:
+// identical integer arithmetic, identical results.  Slice 0 alone writes
+// tokens, status and coder state.  Workgroup b is slice b % P of group
+// b / P: with workgroups placed round-robin on the XCDs, each XCD's L2
+// holds one layer-0 slice plus the hidden layers (3.2 MB of its 4 MB).
+//
+// Exchange of step t: each wave stores its requantised n-tile (32 rows x 32
+// bytes) into the group's buffer of parity t & 1 with agent-coherent (sc1)
+// stores; once they have completed the workgroup publishes
+// flags[slice] = t + 1; wave 0 polls the peers' flags (agent-coherent
+// loads) until each exceeds t; then every thread copies its share of the
+// peers' features into LDS.  A buffer of parity t & 1 is rewritten at step
+// t + 2, by a writer that has seen every peer publish step t + 1, which a
+// peer does only after its reads of step t have completed.  Every wait is
+// bounded (spin_max polls): a workgroup that times out records it and
+// stops publishing and waiting, so that its peers time out too and every
+// workgroup ends; the group's chunks then report SC_STATUS_SYNC_TIMEOUT.
+constexpr int SYNC_SPIN_MAX = 1 << 18;   // ~0.5 s of polls (the default limit)
+constexpr int L0_DEPTH = 16;             // layer-0 weight look-ahead of the split decode (k-steps)
+constexpr int CPOL_SC1 = 16;             // buffer cache policy: sc1, agent-coherent access
+
+// Layer 0's bias for the wave's n-tile into its slot_p0(0) (once per kernel).
+__device__ __forceinline__ void split_params_init(const ModelDev &M, uint32_t *s_par, int nt, int wave, int lane) {
+    uint32_t *blk = s_par + wave * PIPE_SLOTS * Slot<true>::BLK + slot_p0(0) * Slot<true>::BLK;
+    if (lane < Slot<true>::TD) blk[lane] = M.layer[0].par[nt * PAR_DWORDS + lane];
+}
+
+// One MLP evaluation of the group's 32 rows, layer 0 shared (above).  Same
+// contract as mlp_rows_pipe<1, true>; `xbuf` / `flags` are the group's
+// exchange buffers and step flags, s_err the workgroup's timeout flag.
+template <int P, class AposFn>
+__device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
+                                               uint32_t *s_par, AposFn apos, int wave, int lane, uint8_t *xbuf,
+                                               int32_t *flags, int slice, int32_t t, int32_t spin_max,
+                                               int32_t *s_err) {
+    static_assert(P == 4, "one layer-0 n-tile per wave");
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    constexpr int RT = 1;
+    constexpr bool UNI = true;
+    wave = __builtin_amdgcn_readfirstlane(wave);
+    const int voff = lane * 16, g2 = lane >> 5, rl = lane & 31;
+    const int nb0 = 2 * wave;
+    constexpr int BLK = Slot<UNI>::BLK;
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
+    v16i accA[PNT][RT], accB[PNT][RT];
+    constexpr int PPD = ppd<RT>();
+    v4i w[2][PPD][PNT];
+    uint32_t pk[PNT][RT][4];
+    const LayerDev &L0 = M.layer[0];
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(xbuf + (t & 1) * XCH_PAR), (short)0, XCH_PAR, 0x00020000);
+    {
+        const int nt = (HID / 32 / P) * slice + wave;
+        uint32_t prn[Slot<UNI>::LANE];
+        par_fetch<UNI>(M.layer[1].par, nb0, lane, prn);
+        const v16i bias = bias_tile<UNI>(s_parw + slot_p0(0) * BLK, 0, g2);
+        const v16i a0[1] = {gemm_layer0_one<L0_DEPTH>(make_wstream(L0.w, L0.bytes), nt, s_emb, apos, bias, lane)};
+        par_put<UNI>(s_parw + slot_p0(1) * BLK, prn, lane);
+        uint32_t p0[1][4];
+        const RqUni u0 = rq_uni(L0);
+        static_for<4>([&](auto gc) __attribute__((always_inline)) {
+            rq_words_uni<true, 0, 1>(a0, decltype(gc)::value, u0, p0);
+        });
+        const v4i v = {(int)p0[0][0], (int)p0[0][1], (int)p0[0][2], (int)p0[0][3]};
+        const int chunk = nt * 2 + g2;   // hidden order, as pstore_perm
+        *(v4i *)(s_act + pact_off(rl, chunk)) = v;
+        __builtin_amdgcn_raw_buffer_store_b128((v4u)v, xr, rl * XCH_ROW + chunk * 16, 0, CPOL_SC1);
+    }
+    // publish once every wave's stores have completed
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const bool err = *s_err != 0;
+    if (threadIdx.x == 0 && !err) __hip_atomic_store(flags + slice, t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the first hidden layer's first weight fragments while the peers finish
+    {
+        const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
+#pragma unroll
+        for (int s = 0; s < PPD; ++s)
+#pragma unroll
+            for (int j = 0; j < PNT; ++j) w[0][s][j] = wload_s(rs1, voff, ((nb0 + j) * KTH + s) * 1024);
+    }
+    if (wave == 0 && !err) {
+        // at most spin_max polls (none at 0)
+        for (int n = 0;; ++n) {
+            if (n >= spin_max) {
+                if (lane == 0) *s_err = 1;
+                break;
+            }
+            const int32_t f = lane < P && lane != slice
+                                  ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : INT32_MAX;
+            if (__builtin_amdgcn_ballot_w64(f <= t) == 0) break;   // every peer has published step t
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+    // the peers' features: (P - 1) slices x 32 rows x 512 / P bytes, 16-byte pieces
+    {
+        constexpr int CW = 32 / P;                    // 16-byte chunks per row and slice
+        constexpr int ROWP = (P - 1) * CW;            // peer pieces per row
+        constexpr int PER = 32 * ROWP / THREADS;      // pieces per thread
+        static_assert(32 * ROWP % THREADS == 0, "whole pieces per thread");
+        v4i x[PER];
+        int dst[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = u * THREADS + threadIdx.x, row = i / ROWP, c = i % ROWP, q = c / CW;
+            const int chunk = (q + (q >= slice)) * CW + c % CW;
+            x[u] = (v4i)__builtin_amdgcn_raw_buffer_load_b128(xr, row * XCH_ROW + chunk * 16, 0, CPOL_SC1);
+            dst[u] = pact_off(row, chunk);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) *(v4i *)(s_act + dst[u]) = x[u];
+    }
+    __syncthreads();
+    const int last = M.n_layers - 1;
+    if (last == 1) {
+        pipe_hidden<RT, true, UNI, true>(L0, M.layer[1], M.layer[1], s_act, s_parw, 1, accA, accB, w, pk, wave, lane);
+        return;
+    }
+    pipe_hidden<RT, false, UNI, true>(L0, M.layer[1], M.layer[2], s_act, s_parw, 1, accA, accB, w, pk, wave, lane);
+#pragma unroll 1
+    for (int l = 2; l < last; ++l)
+        pipe_hidden<RT, false, UNI>(M.layer[l - 1], M.layer[l], M.layer[l + 1], s_act, s_parw, l, accA, accB, w, pk,
+                                    wave, lane);
+    pipe_hidden<RT, true, UNI>(M.layer[last - 1], M.layer[last], M.layer[last], s_act, s_parw, last, accA, accB, w,
+                               pk, wave, lane);
+}
+
+// P = 1: workgroup b owns chunks [b*R, b*R + R) and never synchronises with
+// another.  P > 1 (RT = 1, pipelined per-tensor core): the split decode
+// above, workgroup b being slice b % P of the group of chunks
+// [(b / P) * 32, (b / P) * 32 + 32).
+template <int RT, int CORE, int P = 1>
 __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uint32_t *__restrict__ words,
                                                            const int64_t *__restrict__ word_off,
                                                            const int32_t *__restrict__ word_cnt,
@@ -260,12 +424,14 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                                                            const int64_t *__restrict__ tok_off,
                                                            int32_t *__restrict__ status,
                                                            DecState *__restrict__ state, int32_t t_begin,
-                                                           int32_t t_end, int64_t n_second) {
+                                                           int32_t t_end, int64_t n_second, uint8_t *xch,
+                                                           int32_t spin_max) {
     // Rows n_chunks - n_second .. n_chunks - 1 each decode a second chunk
     // after their first one ends: row c continues with chunk
     // 2 * n_chunks - 1 - c (the n_second chunks after the launch's own, in
     // reverse order, so that with chunks sorted longest first the longest
     // second chunk follows the shortest first chunk).
+    static_assert(P == 1 || (RT == 1 && CORE == CORE_PIPE_UNI), "the split decode runs 32-row groups on the per-tensor core");
     constexpr bool PIPE = CORE != CORE_PLAIN;
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
@@ -289,11 +455,16 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     // which chunk of the row is current (bit 0: the second one; bit 1: the
     // row has a second chunk) and the step at which it started
     __shared__ int32_t s_cur[R], s_start[R];
-    __shared__ int32_t s_maxlen;
+    __shared__ int32_t s_maxlen, s_xerr;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
-    const int64_t c0 = (int64_t)blockIdx.x * R;
-    if (threadIdx.x == 0) s_maxlen = 0;
+    const int slice = P > 1 ? (int)(blockIdx.x % P) : 0;
+    const int64_t group = blockIdx.x / P, c0 = group * R;
+    const bool writer = slice == 0;   // the workgroup that writes tokens, status and state
+    if (threadIdx.x == 0) {
+        s_maxlen = 0;
+        s_xerr = 0;
+    }
     __syncthreads();
     // The workgroup's step count first, from the lengths alone: a later
     // segment past it returns before reading any coder state, because the
@@ -326,7 +497,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
             cur = state[c].cur;
             start = state[c].start;
         } else if (paired && len1 <= 0) {
-            status[c] = 0;   // an empty first chunk: the second one starts at once
+            if (writer) status[c] = 0;   // an empty first chunk: the second one starts at once
             cur = 1;
         }
         const int64_t cc = cur ? 2 * n_chunks - 1 - c : c;
@@ -363,7 +534,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     }
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    mlp_tile_init<CORE>(M, s_par, wave, lane);
+    if constexpr (P > 1) split_params_init(M, s_par, (HID / 32 / P) * slice + wave, wave, lane);
+    else mlp_tile_init<CORE>(M, s_par, wave, lane);
     __syncthreads();
     if (t_begin > 0) {
         // the context ring: the 64 tokens before t_begin, already written to
@@ -382,13 +554,17 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         __syncthreads();
     }
     for (int32_t t = t_begin; t < t_stop; ++t) {
-        mlp_tile<CORE, RT>(M, s_emb, s_act, s_par,
-                           [&](int r, int p) {
-                               if (t + p < WIN) return emb_off(SOS, 0);
-                               if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
-                               else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
-                           },
-                           wave, lane);
+        auto apos = [&](int r, int p) {
+            if (t + p < WIN) return emb_off(SOS, 0);
+            if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
+            else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
+        };
+        if constexpr (P > 1)
+            mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, wave, lane, xch + group * XCH_GROUP,
+                              (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P, slice, t,
+                              spin_max, &s_xerr);
+        else
+            mlp_tile<CORE, RT>(M, s_emb, s_act, s_par, apos, wave, lane);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
         // _decode_partition (cpu_entropy_coding.py:230-266): every lane of a
         // row computes the row's quantile; the lane whose 16 symbols hold it
@@ -463,11 +639,11 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - s_start[r];
-                        if (pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
+                        if (writer && pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
                         if constexpr (PIPE) s_apos[apos_at(r, 4 * u + k)] = (uint16_t)emb_off(SOS, 0);
                     }
                     if (u == 0) {
-                        status[c] = s_stat[r];
+                        if (writer) status[c] = s_stat[r];
                         const int64_t c2 = 2 * n_chunks - 1 - c;
                         const int32_t cnt = word_cnt[c2];
                         const int64_t woff = word_off[c2];
@@ -491,7 +667,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         // every 64 steps (and at the end) the ring holds the last 64 tokens
         // of each chunk: one wavefront per chunk writes them as one 64-byte
         // run instead of a byte per step
-        if ((t & (WIN - 1)) == WIN - 1 || t == maxlen - 1) {
+        if (writer && ((t & (WIN - 1)) == WIN - 1 || t == maxlen - 1)) {
             const int32_t p = (t & ~(WIN - 1)) + lane;
             for (int r = wave; r < R; r += WAVES) {
                 const int32_t rs = p - s_start[r];
@@ -499,13 +675,20 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
             }
         }
     }
+    if (!writer) return;
+    // a split decode whose exchange timed out: every chunk of the group
+    // (both of a paired row) fails, and a saved state carries the failure
+    // into later segments
+    const bool xerr = P > 1 && s_xerr != 0;
     for (int r = threadIdx.x; r < R; r += THREADS)
         if (c0 + r < n_chunks) {
             const int64_t c = c0 + r;
             const int cur = s_cur[r] & 1;
-            status[cur ? 2 * n_chunks - 1 - c : c] = s_stat[r];
+            const int32_t stat = xerr ? SC_STATUS_SYNC_TIMEOUT : s_stat[r];
+            status[cur ? 2 * n_chunks - 1 - c : c] = stat;
+            if (xerr && (s_cur[r] & 2)) status[cur ? c : 2 * n_chunks - 1 - c] = stat;
             if (t_stop < maxlen)
-                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], s_stat[r], cur, s_start[r]};
+                state[c0 + r] = DecState{s_lower[r], s_range[r], s_point[r], s_rpos[r], stat, cur, s_start[r]};
         }
 }
 

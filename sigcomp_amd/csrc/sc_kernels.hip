@@ -137,6 +137,12 @@ __global__ __launch_bounds__(1024) void k_dec_lengths(const int32_t *__restrict_
     }
 }
 
+// Clears n int32 (the split decode's step flags).  A kernel rather than a
+// memset, so that a caller may capture the call in a HIP graph.
+__global__ __launch_bounds__(256) void k_zero_i32(int32_t *__restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
 // ---- word compaction -----------------------------------------------------
 
 // One wavefront per chunk copies its word_cnt[c] words from its capacity slot
@@ -450,6 +456,9 @@ hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 // Per row tile rt = 3 and 4 are cheapest (38.5 and 39.0 us), rt = 1 the
 // dearest (66.6 us).
 constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 666, 824, 1156, 1561, 2154};
+// Per-step cost of a split decode launch (at most XCH_MAX_GROUPS groups of
+// 32 chunks, SPLIT_P workgroups each), same unit.
+constexpr int DEC_SPLIT_STEP_COST = 330;
 
 // Split `units` row tiles per CU into launch sizes of least summed step cost
 // (largest first, so that they take the longest chunks).
@@ -480,11 +489,12 @@ constexpr int DEC_SEG_STEPS = 256;
 // Decode state of sc_decompress_chunks_static: a file-scope device array
 // (each GPU the library runs on holds its own copy until the process ends)
 // with the coder state of up to SC_STATIC_DEC_MAX_CHUNKS chunks, then the
-// launch plan's four length statistics.  Host code never passes `scratch`
+// launch plan's four length statistics, then the split decode's exchange
+// buffers and flags for XCH_MAX_GROUPS groups.  Host code never passes `scratch`
 // itself (in host code the name is a stand-in, not a device address): the
 // address of the current device's copy comes from hipGetSymbolAddress.
 constexpr int64_t SCRATCH_STATE_BYTES = ((int64_t)SC_STATIC_DEC_MAX_CHUNKS * sizeof(DecState) + 255) / 256 * 256;
-constexpr int64_t SCRATCH_BYTES = SCRATCH_STATE_BYTES + 256;
+constexpr int64_t SCRATCH_BYTES = SCRATCH_STATE_BYTES + 256 + xch_bytes(XCH_MAX_GROUPS);
 __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
@@ -825,9 +835,12 @@ static int64_t dec_state_bytes(int64_t n_chunks) {
     return (n_chunks * (int64_t)sizeof(DecState) + 255) / 256 * 256;
 }
 
+// then the exchange buffers of a split launch
+static int64_t dec_xch_groups(int64_t n_chunks) { return std::min<int64_t>((n_chunks + 31) / 32, XCH_MAX_GROUPS); }
+
 int64_t sc_decompress_workspace_bytes(int64_t n_chunks) {
     if (n_chunks < 0) return -1;
-    return dec_state_bytes(n_chunks) + 256;
+    return dec_state_bytes(n_chunks) + 256 + xch_bytes(dec_xch_groups(n_chunks));
 }
 
 // The launch plan's length statistics on the host (k_dec_lengths' rule):
@@ -845,11 +858,12 @@ static void host_len_stats(const int32_t *len, int64_t n, int64_t g0, int64_t G,
 
 // The decode of sc_decompress_chunks with its buffers given: `state` holds
 // DecState for n_chunks rows, `stat_dev` 4 int32 (used only when
-// lengths_host is NULL).
+// lengths_host is NULL), `xch` xch_bytes(xch_groups) bytes of exchange
+// buffers for a split launch of at most xch_groups groups.
 static int decompress_run(const sc_model *m, const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt,
                           const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
                           int32_t *status, const int32_t *lengths_host, DecState *state, int32_t *stat_dev,
-                          hipStream_t s) {
+                          uint8_t *xch, int64_t xch_groups, hipStream_t s) {
     if (m->dev.pipe == CORE_GENERIC) {
         // step by step over all chunks: the longest chunk bounds the steps
         int32_t st4[4];
@@ -919,15 +933,31 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
     // pairing lengthens the last full-wave launch by the steps its longest
     // pair exceeds its longest chunk; the rt = 1 launch costs the longest
     // leftover chunk's steps
+    // the launch of rt = 1 workgroups that takes what the full waves leave
+    // runs split when its 32-chunk groups fit (SC_HIP_DEC_SPLIT=0: never,
+    // for comparisons)
+    const char *split_env = getenv("SC_HIP_DEC_SPLIT");
+    const bool split_ok = m->dev.pipe == CORE_PIPE_UNI && xch && !(split_env && std::strcmp(split_env, "0") == 0);
+    // polls before a wait for the peers gives up (SC_HIP_DEC_SPIN: a lower
+    // limit, to test the timeout path)
+    const char *spin_env = getenv("SC_HIP_DEC_SPIN");
+    const int32_t spin_max = spin_env ? std::min(std::max(atoi(spin_env), 0), SYNC_SPIN_MAX) : SYNC_SPIN_MAX;
+    auto can_split = [&](int64_t n) {
+        const int64_t groups = (n + 31) / 32;
+        return split_ok && groups <= std::min<int64_t>(xch_groups, XCH_MAX_GROUPS) && groups * SPLIT_P <= cu;
+    };
+    const int left_cost = can_split(left) ? DEC_SPLIT_STEP_COST : DEC_STEP_COST[1];
     const bool pair = can_pair && (int64_t)std::max(0, pair_max - group_max) * DEC_STEP_COST[rt_last] <
-                                      (int64_t)left_max * DEC_STEP_COST[1];
+                                      (int64_t)left_max * left_cost;
     const int64_t maxlen = std::max(len_max, pair ? pair_max : 0);
     if (const char *log = getenv("SC_HIP_DEC_LOG"); log && std::strcmp(log, "1") == 0) {
         std::string rts;
         for (int rt : plan) rts += (rts.empty() ? "" : ",") + std::to_string(rt);
+        const int64_t rest_last = units == 0 ? n_chunks : pair ? 0 : left;
         std::fprintf(stderr, "sc_decompress_chunks: chunks %lld cu %lld plan [%s] leftover %lld %s steps %lld seg %lld\n",
                      (long long)n_chunks, (long long)cu, rts.c_str(), (long long)left,
-                     left == 0 ? "none" : pair ? "paired" : "launch", (long long)maxlen, (long long)seg);
+                     left == 0 ? "none" : pair ? "paired" : rest_last && can_split(rest_last) ? "split launch" : "launch",
+                     (long long)maxlen, (long long)seg);
     }
     int64_t start = 0;
     size_t step = 0;
@@ -935,6 +965,7 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
         const int64_t rest = n_chunks - start;
         int64_t rt, count, n_second = 0;
         unsigned grid;
+        bool split = false;
         if (step < plan.size()) {
             rt = plan[step++];
             count = cu * 32 * rt;
@@ -944,14 +975,38 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
             rt = 1;
             count = rest;
             grid = (unsigned)((rest + 31) / 32);
+            split = can_split(rest);
         }
         const uint32_t *wds = words;
         const int64_t *woff = word_off + start, *toff = tok_off + start;
         const int32_t *wcnt = word_cnt + start, *len = lengths + start;
         int32_t *st = status + start;
         DecState *ds = seg > 0 ? state + start : nullptr;
+        if (split) {
+            // step flags of the grid's groups start at zero (they then hold
+            // the last step each workgroup published, across segments)
+            hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(256), 0, s, (int32_t *)(xch + grid * (int64_t)XCH_GROUP),
+                               (int64_t)grid * SPLIT_P);
+            int rc = check_launch("k_zero_i32");
+            if (rc) return rc;
+        }
         for (int64_t tb = 0; tb == 0 || (seg > 0 && tb < maxlen); tb += (seg > 0 ? seg : INT32_MAX)) {
             const int32_t t0 = (int32_t)tb, t1 = seg > 0 ? (int32_t)std::min<int64_t>(INT32_MAX, tb + seg) : INT32_MAX;
+            if (split) {
+                const hipError_t e = launch_decompress_split(m->dev, grid, s, wds, woff, wcnt, len, count, tokens, toff,
+                                                             st, ds, t0, t1, xch, spin_max);
+                if (e == hipSuccess) {
+                    int rc = check_launch("k_decompress (split)");
+                    if (rc) return rc;
+                    continue;
+                }
+                // a device that cannot hold the whole grid at once: the
+                // decode runs unsplit (found at the first segment; a later
+                // failure is an error)
+                (void)hipGetLastError();
+                if (tb > 0 || e != hipErrorCooperativeLaunchTooLarge) return hip_fail(e, "k_decompress (split)");
+                split = false;
+            }
             switch (rt) {
 #define SC_DEC_CASE(N)                                                                                        \
     case N:                                                                                                   \
@@ -984,8 +1039,9 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     DeviceGuard guard(m->device);
     DecState *state = (DecState *)workspace;
     int32_t *stat_dev = (int32_t *)((char *)workspace + dec_state_bytes(n_chunks));
+    uint8_t *xch = (uint8_t *)workspace + dec_state_bytes(n_chunks) + 256;
     return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
-                          state, stat_dev, as_stream(stream));
+                          state, stat_dev, xch, dec_xch_groups(n_chunks), as_stream(stream));
 }
 
 int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const int64_t *word_off,
@@ -1008,11 +1064,13 @@ int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const 
     void *base = scratch_ptr(m->device, &rc);
     if (!base) return rc;
     // every DecState is written by a segment before a later one reads it and
-    // the statistics are written before they are read: nothing to clear
+    // the statistics are written before they are read; a split launch clears
+    // its step flags itself (a kernel, no memset)
     DecState *state = (DecState *)base;
     int32_t *stat_dev = (int32_t *)((char *)base + SCRATCH_STATE_BYTES);
+    uint8_t *xch = (uint8_t *)base + SCRATCH_STATE_BYTES + 256;
     return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
-                          state, stat_dev, as_stream(stream));
+                          state, stat_dev, xch, XCH_MAX_GROUPS, as_stream(stream));
 }
 
 }  // extern "C"

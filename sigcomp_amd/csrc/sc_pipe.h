@@ -296,7 +296,10 @@ __device__ __forceinline__ void pipe_schedule() {
 // slot_p1(l) = its parameters, slot_p0(l+1) = the next layer's pass-0
 // parameters, region A = this layer's pass 0 (visible), w[0][*] = the next
 // layer's first k-steps.  Both passes' GEMMs start from their bias tiles.
-template <int RT, bool LASTL, bool UNI>
+// FRESH: the whole previous layer is already in regions A and B (visible),
+// accB holds nothing to requantise (the first layer after a layer 0 whose
+// features were gathered from several workgroups).
+template <int RT, bool LASTL, bool UNI, bool FRESH = false>
 __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &L, const LayerDev &Ln, uint8_t *s_act,
                                             uint32_t *s_parw, int l, v16i (&accA)[PNT][RT],
                                             v16i (&accB)[PNT][RT], v4i (&w)[2][ppd<RT>()][PNT],
@@ -351,8 +354,8 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
                 w[(vp / PPD) & 1][vp % PPD][j] = wload_s(rsn, voff, ((nb0 + j) * KTH + kn) * 1024);
         }
         // side work: parameters one step ahead, then requantised words
-        constexpr int VA = v < 8 ? 12 : (!LASTL && v >= 16 ? 6 : 0);
-        if constexpr (v < 8) {
+        constexpr int VA = v < 8 ? (FRESH ? 0 : 12) : (!LASTL && v >= 16 ? 6 : 0);
+        if constexpr (v < 8 && !FRESH) {
             constexpr int j = v / 4, gg = v % 4;
             if constexpr (UNI) {
                 rq_words_uni<true, 0, RT>(accB[j], gg, up, pk[j]);
@@ -390,14 +393,14 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (v == 7) {
             // layer l-1 pass 1 -> region B; this layer's pass-1 and the next
-            // layer's pass-0 parameters -> LDS
-            pstore_perm<RT>(pk, nb1, s_act, lane);
+            // layer's pass-0 parameters -> LDS (the wave's own slots)
+            if constexpr (!FRESH) pstore_perm<RT>(pk, nb1, s_act, lane);
             if constexpr (!LASTL) {
                 par_put<UNI>(cur1, pr1, lane);
                 par_put<UNI>(next0, prn, lane);
                 if constexpr (!UNI) pp = rq_par(cur0, 0, 0, g);   // first parameters of the pass-0 requantisation
             }
-            __syncthreads();
+            if constexpr (!FRESH) __syncthreads();
             read_b<RT>(s_act, bbase, 8, b[0]);
         }
     });
@@ -411,6 +414,59 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
         pstore_perm<RT>(pk, nb0, s_act, lane);
     }
     __syncthreads();
+}
+
+// Layer 0 of ONE n-tile for one row tile (32 rows), the operands laid out as
+// in gemm_layer0_map, with the weight fragments loaded D k-steps ahead: a
+// wave keeps D fragments (D KB) in flight, as many as a wave of
+// gemm_layer0_map keeps over its four n-tiles.  The accumulator starts from
+// `init`.  Position p's table address is read at the first k-step of
+// position p - 1, its first B fragment at the last one.  The look-ahead
+// stops at the n-tile's last k-tile.
+template <int D, class AposFn>
+__device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, const uint8_t *s_emb, AposFn apos,
+                                                const v16i &init, int lane) {
+    constexpr int KS = EDIM / 32;   // k-steps per position
+    static_assert(D % KS == 0 && KT0 % D == 0 && KT0 / D >= 2, "prefetch depth: whole positions dividing the k-tiles");
+    const int voff = nt * KT0 * 1024 + lane * 16;
+    v4i w[D];
+#pragma unroll
+    for (int s = 0; s < D; ++s) w[s] = wload(ws, voff, s);
+    const int rl = lane & 31, kg = (lane >> 5) << 4;
+    int ea = apos(rl, 0) + kg, an = 0;
+    v4i b[2];
+    b[0] = *(const v4i *)(s_emb + ea);
+    v16i acc;
+    // D k-steps (D / KS positions) from position p0; FIRST starts from
+    // init, LAST issues no more weight loads
+    auto body = [&](int p0, auto firstc, auto lastc) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(firstc)::value, LAST = decltype(lastc)::value;
+        static_for<D>([&](auto sc) __attribute__((always_inline)) {
+            constexpr int s = decltype(sc)::value, q = s % KS;
+            const int p = p0 + s / KS;
+            // this step's weights: issued D loads ago (fewer are outstanding
+            // once LAST stops issuing)
+            if constexpr (LAST) wait_counts<D - 1 - s, 0>();
+            else wait_counts<D - 1, 0>();
+            if constexpr (q == 0) {
+                if (p + 1 < WIN) an = apos(rl, p + 1);
+            }
+            if constexpr (q + 1 < KS) {
+                b[(s + 1) & 1] = *(const v4i *)(s_emb + ea + (q + 1) * 32);
+            } else if (!LAST || s + 1 < D) {
+                ea = an + kg;
+                b[(s + 1) & 1] = *(const v4i *)(s_emb + ea);
+            }
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[s], b[s & 1], FIRST && s == 0 ? init : acc, 0, 0, 0);
+            if constexpr (!LAST) w[s] = wload(ws, voff, p0 * KS + s + D);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    body(0, std::true_type{}, std::false_type{});
+#pragma unroll 1
+    for (int p0 = D / KS; p0 < WIN - D / KS; p0 += D / KS) body(p0, std::false_type{}, std::false_type{});
+    body(WIN - D / KS, std::false_type{}, std::true_type{});
+    return acc;
 }
 
 // One MLP evaluation of R = 32*RT rows (RT <= 4), same contract as mlp_rows

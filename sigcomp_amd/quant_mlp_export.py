@@ -445,6 +445,9 @@ class QuantMLPCompression(ReadFramingMixin):
             torch.cuda.current_stream().synchronize()
         st = h_status.numpy()
         if st.any():
+            bad = np.flatnonzero(st)
+            if (st[bad] == _hip.SC_STATUS_SYNC_TIMEOUT).any():
+                raise RuntimeError("GPU decode: the workgroups sharing a decode step timed out waiting for each other")
             raise ValueError("invalid range stream or mismatching entropy model in chunk "
-                             f"{int(order[np.flatnonzero(st)[0]])}")
+                             f"{int(order[bad[0]])}")
         return h_tokens.numpy()[:n_tokens], tok_off

@@ -593,7 +593,7 @@ def test_decompress_rejects_pairing_of_long_leftovers(codecs, capfd, monkeypatch
     _set_dec_env(monkeypatch, None)
     back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
     log = capfd.readouterr().err
-    assert "leftover 40 launch" in log, log
+    assert "leftover 40 split launch" in log, log
     assert np.array_equal(back, tokens)
 
 
@@ -657,6 +657,105 @@ def test_decompress_status_survives_later_segments(codecs, monkeypatch):
         keep = np.ones(len(back), bool)
         keep[tok_off[40]:tok_off[40] + 10] = False
         assert np.array_equal(back[keep], tokens[keep])
+
+
+def _random_chunks(codec, n, hi, seed):
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(1, hi + 1, n).astype(np.int32)
+    tokens = rng.integers(0, 60, int(lengths.sum())).astype(np.uint8)
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    return tokens, lengths, words, woff, wcnt
+
+
+@pytest.mark.parametrize("n,seg", [(1, None), (3, 64), (33, None), (675, None), (675, 64), (675, 0), (2048, None)])
+def test_split_decode_matches_unsplit(codecs, capfd, monkeypatch, n, seg):
+    """Launches of at most 64 groups of 32 chunks decode split (four
+    workgroups per group share layer 0 and exchange its features every
+    step): one chunk, a partial group, two groups, 22 groups (the c1 case)
+    over 256-step and 64-step segments and one launch, and the largest split
+    launch.  Tokens equal the input and the unsplit decode's
+    (SC_HIP_DEC_SPLIT=0)."""
+    codec = codecs["lossless"]
+    tokens, lengths, words, woff, wcnt = _random_chunks(codec, n, 700, n)
+    _set_dec_env(monkeypatch, seg)
+    capfd.readouterr()
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "split launch" in log, log
+    assert np.array_equal(back, tokens)
+    monkeypatch.setenv("SC_HIP_DEC_SPLIT", "0")
+    back0, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "split" not in log and "launch" in log, log
+    assert np.array_equal(back0, tokens)
+
+
+def test_split_decode_not_used_beyond_64_groups(codecs, capfd, monkeypatch):
+    """2,049 chunks make 65 groups, more than a split launch holds: one
+    unsplit launch of 32-chunk workgroups."""
+    codec = codecs["lossless"]
+    tokens, lengths, words, woff, wcnt = _random_chunks(codec, 2049, 200, 3)
+    _set_dec_env(monkeypatch, None)
+    capfd.readouterr()
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "leftover 2049 launch" in log, log
+    assert np.array_equal(back, tokens)
+
+
+@pytest.mark.parametrize("lossy", [False, True])
+def test_split_decode_matches_oracle(codecs, oracle_mod, oracle_models, lossy):
+    """Split decode of 40 chunks (two groups, the second partial) with the
+    lossless and the lossy model: every chunk's tokens equal the oracle's
+    decode of the same words."""
+    name = "lossy" if lossy else "lossless"
+    codec = codecs[name]
+    tokens, lengths, words, woff, wcnt = _random_chunks(codec, 40, 300, 11 + lossy)
+    back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths)
+    assert not status.any()
+    enc = [words[woff[c]:woff[c] + wcnt[c]].astype("<u4").tobytes() for c in range(len(lengths))]
+    ref = oracle_mod.decompress_chunks(oracle_models[name], enc, lengths)
+    for c in range(len(lengths)):
+        assert np.array_equal(back[tok_off[c]:tok_off[c] + lengths[c]], ref[c]), c
+
+
+def test_split_decode_corrupt_chunks(codecs, monkeypatch):
+    """Corrupt chunks in both groups of a split decode over 64-step
+    segments: each reports an invalid stream, every other chunk decodes."""
+    codec = codecs["lossless"]
+    tokens, lengths, words, woff, wcnt = _random_chunks(codec, 70, 400, 5)
+    bad = [0, 33, 69]
+    words = np.concatenate([words, np.full(2, 0xFFFFFFFF, np.uint32)])
+    woff, wcnt = woff.copy(), wcnt.copy()
+    woff[bad], wcnt[bad] = len(words) - 2, 2
+    monkeypatch.setenv("SC_HIP_DEC_SEG", "64")
+    back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths)
+    expect = np.zeros(len(lengths), np.int32)
+    expect[bad] = 2   # SC_STATUS_INVALID_STREAM
+    assert np.array_equal(status, expect)
+    for i in range(len(lengths)):
+        if i not in bad:
+            s = slice(tok_off[i], tok_off[i] + lengths[i])
+            assert np.array_equal(back[s], tokens[s]), i
+
+
+def test_split_decode_timeout_reports_status(codecs, monkeypatch):
+    """With a spin limit of 0 polls (SC_HIP_DEC_SPIN=0; the default is
+    2**18) every wait of a split decode gives up at once: every chunk of
+    every group reports SC_STATUS_SYNC_TIMEOUT, also through later step
+    segments, and decompress_flat raises RuntimeError.  The kernels end
+    normally, and the next decode is correct."""
+    codec = codecs["lossless"]
+    tokens, lengths, words, woff, wcnt = _random_chunks(codec, 40, 300, 9)
+    monkeypatch.setenv("SC_HIP_DEC_SPIN", "0")
+    monkeypatch.setenv("SC_HIP_DEC_SEG", "64")
+    _, status, _ = _decode_direct(codec, words, woff, wcnt, lengths)
+    assert (status == 4).all(), status   # SC_STATUS_SYNC_TIMEOUT
+    with pytest.raises(RuntimeError, match="timed out"):
+        codec.decompress_flat(words, woff, wcnt, lengths)
+    monkeypatch.delenv("SC_HIP_DEC_SPIN")
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    assert np.array_equal(back, tokens)
 
 
 def test_mfma_burn_hook_computes_its_products():
