@@ -212,7 +212,7 @@ int sc_mfma_burn_i8(const int8_t *ops, int32_t iters, int32_t n_groups, int32_t 
 /* Bytes of device workspace sc_decompress_chunks needs for n_chunks chunks:
  * the coder state of every chunk between step segments (40 bytes per chunk),
  * the launch plan's four length statistics, and the exchange buffers of a
- * split decode (32 KiB per 32 chunks, at most 64 such groups, and 16 bytes of
+ * split decode (32 KiB per 32 chunks, at most 64 such groups, and 32 bytes of
  * step flags per group), each part 256-byte aligned. */
 int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
 
@@ -233,10 +233,11 @@ int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
  * descending length (as QuantMLPCompression passes them) give the shortest
  * schedule: the shortest chunks are then left over after the full waves of
  * workgroups and follow the shortest chunks of the last full wave in the
- * same rows.  A launch of few 32-chunk groups (at most a quarter of the
- * CUs) runs split: four workgroups per group share layer 0 and wait for
- * each other every step (a cooperative launch, so all are resident; a
- * bounded wait, SC_STATUS_SYNC_TIMEOUT when it expires).  Replaces
+ * same rows.  A launch of at most 64 groups of 32 chunks runs split: 8
+ * workgroups per group (4 when the CUs cannot hold 8) share layer 0 and
+ * wait for each other every step (a cooperative launch, so all are
+ * resident; a bounded wait, SC_STATUS_SYNC_TIMEOUT when it expires).
+ * Replaces
  * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
  * (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */

@@ -1,10 +1,10 @@
 // sc_dec_split.hip -- the split decode of small batches (k_decompress with
-// SPLIT_P workgroups per 32-chunk group sharing layer 0).
+// 4 or 8 workgroups per 32-chunk group sharing layer 0).
 #include "sc_kernels.h"
 
 namespace sc {
 
-hipError_t launch_decompress_split(const ModelDev &M, unsigned groups, hipStream_t s, const uint32_t *words,
+hipError_t launch_decompress_split(const ModelDev &M, int p, unsigned groups, hipStream_t s, const uint32_t *words,
                                    const int64_t *woff, const int32_t *wcnt, const int32_t *len, int64_t count,
                                    uint8_t *tokens, const int64_t *toff, int32_t *st, DecState *state,
                                    int32_t t_begin, int32_t t_end, uint8_t *xch, int32_t spin_max) {
@@ -14,8 +14,9 @@ hipError_t launch_decompress_split(const ModelDev &M, unsigned groups, hipStream
                     (void *)&t_end, (void *)&n_second, (void *)&xch, (void *)&spin_max};
     // cooperative: every workgroup of the grid is resident at once (the
     // groups' workgroups wait for each other)
-    return hipLaunchCooperativeKernel((const void *)k_decompress<1, CORE_PIPE_UNI, SPLIT_P>,
-                                      dim3(groups * SPLIT_P), dim3(THREADS), args, 0, s);
+    const void *kern = p == 8 ? (const void *)k_decompress<1, CORE_PIPE_UNI, 8>
+                              : (const void *)k_decompress<1, CORE_PIPE_UNI, 4>;
+    return hipLaunchCooperativeKernel(kern, dim3(groups * (p == 8 ? 8 : 4)), dim3(THREADS), args, 0, s);
 }
 
 }  // namespace sc

@@ -27,17 +27,17 @@ struct DecState {
     int32_t rpos, stat, cur, start;
 };
 
-// Split decode (small batches): SPLIT_P workgroups per 32-chunk group share
-// layer 0 (see k_decompress).  Per group the exchange workspace holds two
-// parity buffers of 32 rows x 512 feature bytes; after the buffers of all
-// groups come SPLIT_P int32 step flags per group.
-constexpr int SPLIT_P = 4;
+// Split decode (small batches): P = 4 or 8 workgroups per 32-chunk group
+// share layer 0 (see k_decompress).  Per group the exchange workspace holds
+// two parity buffers of 32 rows x 512 feature bytes; after the buffers of
+// all groups come P int32 step flags per group (room for SPLIT_P_MAX).
+constexpr int SPLIT_P_MAX = 8;
 constexpr int XCH_ROW = HID;                 // bytes per row of an exchange buffer
 constexpr int XCH_PAR = 32 * XCH_ROW;        // one parity buffer
 constexpr int XCH_GROUP = 2 * XCH_PAR;       // both parities of one group
 constexpr int XCH_MAX_GROUPS = 64;           // 64 x 4 workgroups fill the 256 CUs
 constexpr int64_t xch_bytes(int64_t groups) {
-    return groups * XCH_GROUP + (groups * SPLIT_P * 4 + 255) / 256 * 256;
+    return groups * XCH_GROUP + (groups * SPLIT_P_MAX * 4 + 255) / 256 * 256;
 }
 
 // Host launchers (stream-ordered, no error check: the caller checks
@@ -51,13 +51,14 @@ template <int RT>
 void launch_decompress(const ModelDev &M, unsigned grid, hipStream_t s, const uint32_t *words, const int64_t *woff,
                        const int32_t *wcnt, const int32_t *len, int64_t count, uint8_t *tokens, const int64_t *toff,
                        int32_t *st, DecState *state, int32_t t_begin, int32_t t_end, int64_t n_second);
-// The split decode of `groups` 32-chunk groups (pipelined per-tensor core
-// only): a cooperative launch of groups * SPLIT_P workgroups, so that all
-// are resident at once; returns the launch's error (the caller falls back
-// when the device cannot hold them).  `xch` = xch_bytes(groups) bytes, the
-// flags zeroed before the first step segment of a call; each wait for the
-// peers gives up after spin_max polls (SYNC_SPIN_MAX).
-hipError_t launch_decompress_split(const ModelDev &M, unsigned groups, hipStream_t s, const uint32_t *words,
+// The split decode of `groups` 32-chunk groups with p = 4 or 8 workgroups
+// each (pipelined per-tensor core only): a cooperative launch of groups * p
+// workgroups, so that all are resident at once; returns the launch's error
+// (the caller falls back when the device cannot hold them).  `xch` =
+// xch_bytes(groups) bytes, the flags zeroed before the first step segment
+// of a call; each wait for the peers gives up after spin_max polls
+// (SYNC_SPIN_MAX).
+hipError_t launch_decompress_split(const ModelDev &M, int p, unsigned groups, hipStream_t s, const uint32_t *words,
                                    const int64_t *woff, const int32_t *wcnt, const int32_t *len, int64_t count,
                                    uint8_t *tokens, const int64_t *toff, int32_t *st, DecState *state,
                                    int32_t t_begin, int32_t t_end, uint8_t *xch, int32_t spin_max);
@@ -280,17 +281,20 @@ __device__ __forceinline__ uint64_t dec_init_point(const uint32_t *w, int cnt, i
 // With few chunks a decode has few 32-row workgroups, and each step streams
 // the whole model (6.2 MB) through one CU's vector L1 for 32 rows.  In the
 // split decode the P workgroups of a group each compute 512 / P of layer
-// 0's features (n-tile 16 / P * slice + wave: one n-tile per wave at
-// P = 4), exchange them through memory, and then all of them run the
-// hidden layers, the output layer and the decoder step on the same data:
-// identical integer arithmetic, identical results.  Slice 0 alone writes
-// tokens, status and coder state.  Workgroup b is slice b % P of group
-// b / P: with workgroups placed round-robin on the XCDs, each XCD's L2
-// holds one layer-0 slice plus the hidden layers (3.2 MB of its 4 MB).
+// 0's features (n-tiles 16 / P * slice ..: at P = 4 one n-tile per wave, at
+// P = 8 two, each over half of the window positions by a pair of waves whose
+// partial sums meet in LDS), exchange them through memory, and then all of
+// them run the hidden layers, the output layer and the decoder step on the
+// same data: identical integer arithmetic, identical results.  Slice 0
+// alone writes tokens, status and coder state.  Workgroup b is slice b % P
+// of group b / P: with workgroups placed round-robin on the 8 XCDs, each
+// XCD's L2 holds one layer-0 slice (P = 8) or two (P = 4) plus the hidden
+// layers.
 //
-// Exchange of step t: each wave stores its requantised n-tile (32 rows x 32
-// bytes) into the group's buffer of parity t & 1 with agent-coherent (sc1)
-// stores; once they have completed the workgroup publishes
+// Exchange of step t: each n-tile's requantised features (32 rows x 32
+// bytes) are stored into the group's buffer of parity t & 1 with
+// agent-coherent (sc1) stores; once they have completed the workgroup
+// publishes
 // flags[slice] = t + 1; wave 0 polls the peers' flags (agent-coherent
 // loads) until each exceeds t; then every thread copies its share of the
 // peers' features into LDS.  A buffer of parity t & 1 is rewritten at step
@@ -304,6 +308,8 @@ constexpr int L0_DEPTH = 16;             // layer-0 weight look-ahead of the spl
 constexpr int CPOL_SC1 = 16;             // buffer cache policy: sc1, agent-coherent access
 
 // Layer 0's bias for the wave's n-tile into its slot_p0(0) (once per kernel).
+template <int P>
+__device__ __forceinline__ int split_ntile(int slice, int wave) { return 16 / P * slice + wave % (16 / P); }
 __device__ __forceinline__ void split_params_init(const ModelDev &M, uint32_t *s_par, int nt, int wave, int lane) {
     uint32_t *blk = s_par + wave * PIPE_SLOTS * Slot<true>::BLK + slot_p0(0) * Slot<true>::BLK;
     if (lane < Slot<true>::TD) blk[lane] = M.layer[0].par[nt * PAR_DWORDS + lane];
@@ -311,13 +317,16 @@ __device__ __forceinline__ void split_params_init(const ModelDev &M, uint32_t *s
 
 // One MLP evaluation of the group's 32 rows, layer 0 shared (above).  Same
 // contract as mlp_rows_pipe<1, true>; `xbuf` / `flags` are the group's
-// exchange buffers and step flags, s_err the workgroup's timeout flag.
+// exchange buffers and step flags, s_err the workgroup's timeout flag,
+// s_red (P = 8) 2 x 4 KB of LDS for the partial sums.
 template <int P, class AposFn>
 __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
                                                uint32_t *s_par, AposFn apos, int wave, int lane, uint8_t *xbuf,
                                                int32_t *flags, int slice, int32_t t, int32_t spin_max,
-                                               int32_t *s_err) {
-    static_assert(P == 4, "one layer-0 n-tile per wave");
+                                               int32_t *s_err, int32_t *s_red) {
+    static_assert(P == 4 || P == 8, "one or two layer-0 n-tiles per wave pair");
+    constexpr int NTW = 16 / P;           // layer-0 n-tiles of the workgroup
+    constexpr int KSPLIT = WAVES / NTW;   // waves per n-tile, each over WIN / KSPLIT positions
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     constexpr int RT = 1;
     constexpr bool UNI = true;
@@ -334,21 +343,40 @@ __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t 
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *)(xbuf + (t & 1) * XCH_PAR), (short)0, XCH_PAR, 0x00020000);
     {
-        const int nt = (HID / 32 / P) * slice + wave;
+        const int nt = split_ntile<P>(slice, wave), kp = wave / NTW;   // n-tile, part of the window
         uint32_t prn[Slot<UNI>::LANE];
         par_fetch<UNI>(M.layer[1].par, nb0, lane, prn);
         const v16i bias = bias_tile<UNI>(s_parw + slot_p0(0) * BLK, 0, g2);
-        const v16i a0[1] = {gemm_layer0_one<L0_DEPTH>(make_wstream(L0.w, L0.bytes), nt, s_emb, apos, bias, lane)};
+        const v16i zero = {};
+        constexpr int NW = WIN / KSPLIT;
+        v16i a0[1] = {gemm_layer0_one<L0_DEPTH, NW>(make_wstream(L0.w, L0.bytes), nt, kp * NW, s_emb, apos,
+                                                    kp == 0 ? bias : zero, lane)};
         par_put<UNI>(s_parw + slot_p0(1) * BLK, prn, lane);
-        uint32_t p0[1][4];
-        const RqUni u0 = rq_uni(L0);
-        static_for<4>([&](auto gc) __attribute__((always_inline)) {
-            rq_words_uni<true, 0, 1>(a0, decltype(gc)::value, u0, p0);
-        });
-        const v4i v = {(int)p0[0][0], (int)p0[0][1], (int)p0[0][2], (int)p0[0][3]};
-        const int chunk = nt * 2 + g2;   // hidden order, as pstore_perm
-        *(v4i *)(s_act + pact_off(rl, chunk)) = v;
-        __builtin_amdgcn_raw_buffer_store_b128((v4u)v, xr, rl * XCH_ROW + chunk * 16, 0, CPOL_SC1);
+        if constexpr (KSPLIT > 1) {
+            // the second half's partial sums -> the first half's wave
+            static_assert(KSPLIT == 2, "two waves per n-tile");
+            int32_t *red = s_red + (wave % NTW) * 16 * 64 + lane;
+            if (kp == 1) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) red[e * 64] = a0[0][e];
+            }
+            __syncthreads();
+            if (kp == 0) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) a0[0][e] = (int)((uint32_t)a0[0][e] + (uint32_t)red[e * 64]);
+            }
+        }
+        if (kp == 0) {
+            uint32_t p0[1][4];
+            const RqUni u0 = rq_uni(L0);
+            static_for<4>([&](auto gc) __attribute__((always_inline)) {
+                rq_words_uni<true, 0, 1>(a0, decltype(gc)::value, u0, p0);
+            });
+            const v4i v = {(int)p0[0][0], (int)p0[0][1], (int)p0[0][2], (int)p0[0][3]};
+            const int chunk = nt * 2 + g2;   // hidden order, as pstore_perm
+            *(v4i *)(s_act + pact_off(rl, chunk)) = v;
+            __builtin_amdgcn_raw_buffer_store_b128((v4u)v, xr, rl * XCH_ROW + chunk * 16, 0, CPOL_SC1);
+        }
     }
     // publish once every wave's stores have completed
     __builtin_amdgcn_s_waitcnt(0);
@@ -382,17 +410,18 @@ __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t 
     {
         constexpr int CW = 32 / P;                    // 16-byte chunks per row and slice
         constexpr int ROWP = (P - 1) * CW;            // peer pieces per row
-        constexpr int PER = 32 * ROWP / THREADS;      // pieces per thread
-        static_assert(32 * ROWP % THREADS == 0, "whole pieces per thread");
+        constexpr int PER = (32 * ROWP + THREADS - 1) / THREADS;   // pieces per thread (the last in part)
         v4i x[PER];
         int dst[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const int i = u * THREADS + threadIdx.x, row = i / ROWP, c = i % ROWP, q = c / CW;
+            const int i = min(u * THREADS + (int)threadIdx.x, 32 * ROWP - 1);
+            const int row = i / ROWP, c = i % ROWP, q = c / CW;
             const int chunk = (q + (q >= slice)) * CW + c % CW;
             x[u] = (v4i)__builtin_amdgcn_raw_buffer_load_b128(xr, row * XCH_ROW + chunk * 16, 0, CPOL_SC1);
             dst[u] = pact_off(row, chunk);
         }
+        // (threads past the last piece repeat it: the same bytes to the same place)
 #pragma unroll
         for (int u = 0; u < PER; ++u) *(v4i *)(s_act + dst[u]) = x[u];
     }
@@ -432,6 +461,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     // reverse order, so that with chunks sorted longest first the longest
     // second chunk follows the shortest first chunk).
     static_assert(P == 1 || (RT == 1 && CORE == CORE_PIPE_UNI), "the split decode runs 32-row groups on the per-tensor core");
+    static_assert(P == 1 || P == 4 || P == 8, "split decode: 4 or 8 workgroups per group");
     constexpr bool PIPE = CORE != CORE_PLAIN;
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
@@ -456,6 +486,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     // row has a second chunk) and the step at which it started
     __shared__ int32_t s_cur[R], s_start[R];
     __shared__ int32_t s_maxlen, s_xerr;
+    __shared__ int32_t s_red[P == 8 ? 2 * 16 * 64 : 1];   // partial layer-0 sums of the split decode
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q4 = lane >> 4, u = lane & 15;
     const int slice = P > 1 ? (int)(blockIdx.x % P) : 0;
@@ -534,7 +565,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     }
     load_emb_lds(M.emb, s_emb);
     load_lut_lds(M.lut, s_lut);
-    if constexpr (P > 1) split_params_init(M, s_par, (HID / 32 / P) * slice + wave, wave, lane);
+    if constexpr (P > 1) split_params_init(M, s_par, split_ntile<P>(slice, wave), wave, lane);
     else mlp_tile_init<CORE>(M, s_par, wave, lane);
     __syncthreads();
     if (t_begin > 0) {
@@ -562,7 +593,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         if constexpr (P > 1)
             mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, wave, lane, xch + group * XCH_GROUP,
                               (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P, slice, t,
-                              spin_max, &s_xerr);
+                              spin_max, &s_xerr, s_red);
         else
             mlp_tile<CORE, RT>(M, s_emb, s_act, s_par, apos, wave, lane);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.

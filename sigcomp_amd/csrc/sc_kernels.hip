@@ -457,8 +457,8 @@ hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 // dearest (66.6 us).
 constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 666, 824, 1156, 1561, 2154};
 // Per-step cost of a split decode launch (at most XCH_MAX_GROUPS groups of
-// 32 chunks, SPLIT_P workgroups each), same unit.
-constexpr int DEC_SPLIT_STEP_COST = 330;
+// 32 chunks) with 4 and 8 workgroups per group, same unit.
+constexpr int DEC_SPLIT_STEP_COST_P4 = 282, DEC_SPLIT_STEP_COST_P8 = 256;
 
 // Split `units` row tiles per CU into launch sizes of least summed step cost
 // (largest first, so that they take the longest chunks).
@@ -934,19 +934,25 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
     // pair exceeds its longest chunk; the rt = 1 launch costs the longest
     // leftover chunk's steps
     // the launch of rt = 1 workgroups that takes what the full waves leave
-    // runs split when its 32-chunk groups fit (SC_HIP_DEC_SPLIT=0: never,
-    // for comparisons)
+    // runs split when its 32-chunk groups fit: 8 workgroups per group when
+    // the CUs hold them, else 4 (SC_HIP_DEC_SPLIT=0: never, 4 or 8: only
+    // that split, for comparisons)
     const char *split_env = getenv("SC_HIP_DEC_SPLIT");
-    const bool split_ok = m->dev.pipe == CORE_PIPE_UNI && xch && !(split_env && std::strcmp(split_env, "0") == 0);
+    const int split_force = split_env ? atoi(split_env) : -1;
+    const bool split_ok = m->dev.pipe == CORE_PIPE_UNI && xch && split_force != 0;
     // polls before a wait for the peers gives up (SC_HIP_DEC_SPIN: a lower
     // limit, to test the timeout path)
     const char *spin_env = getenv("SC_HIP_DEC_SPIN");
     const int32_t spin_max = spin_env ? std::min(std::max(atoi(spin_env), 0), SYNC_SPIN_MAX) : SYNC_SPIN_MAX;
-    auto can_split = [&](int64_t n) {
+    auto split_p = [&](int64_t n) {   // workgroups per group of a split launch of n chunks (0: unsplit)
         const int64_t groups = (n + 31) / 32;
-        return split_ok && groups <= std::min<int64_t>(xch_groups, XCH_MAX_GROUPS) && groups * SPLIT_P <= cu;
+        if (!split_ok || groups > std::min<int64_t>(xch_groups, XCH_MAX_GROUPS)) return 0;
+        if (split_force != 4 && groups * 8 <= cu) return 8;
+        if (split_force != 8 && groups * 4 <= cu) return 4;
+        return 0;
     };
-    const int left_cost = can_split(left) ? DEC_SPLIT_STEP_COST : DEC_STEP_COST[1];
+    const int p_left = split_p(left);
+    const int left_cost = p_left == 8 ? DEC_SPLIT_STEP_COST_P8 : p_left == 4 ? DEC_SPLIT_STEP_COST_P4 : DEC_STEP_COST[1];
     const bool pair = can_pair && (int64_t)std::max(0, pair_max - group_max) * DEC_STEP_COST[rt_last] <
                                       (int64_t)left_max * left_cost;
     const int64_t maxlen = std::max(len_max, pair ? pair_max : 0);
@@ -954,9 +960,10 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
         std::string rts;
         for (int rt : plan) rts += (rts.empty() ? "" : ",") + std::to_string(rt);
         const int64_t rest_last = units == 0 ? n_chunks : pair ? 0 : left;
+        const int pl = rest_last ? split_p(rest_last) : 0;
         std::fprintf(stderr, "sc_decompress_chunks: chunks %lld cu %lld plan [%s] leftover %lld %s steps %lld seg %lld\n",
                      (long long)n_chunks, (long long)cu, rts.c_str(), (long long)left,
-                     left == 0 ? "none" : pair ? "paired" : rest_last && can_split(rest_last) ? "split launch" : "launch",
+                     left == 0 ? "none" : pair ? "paired" : pl == 8 ? "split launch p8" : pl == 4 ? "split launch p4" : "launch",
                      (long long)maxlen, (long long)seg);
     }
     int64_t start = 0;
@@ -965,7 +972,7 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
         const int64_t rest = n_chunks - start;
         int64_t rt, count, n_second = 0;
         unsigned grid;
-        bool split = false;
+        int split = 0;   // workgroups per group of a split launch
         if (step < plan.size()) {
             rt = plan[step++];
             count = cu * 32 * rt;
@@ -975,7 +982,7 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
             rt = 1;
             count = rest;
             grid = (unsigned)((rest + 31) / 32);
-            split = can_split(rest);
+            split = split_p(rest);
         }
         const uint32_t *wds = words;
         const int64_t *woff = word_off + start, *toff = tok_off + start;
@@ -986,15 +993,15 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
             // step flags of the grid's groups start at zero (they then hold
             // the last step each workgroup published, across segments)
             hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(256), 0, s, (int32_t *)(xch + grid * (int64_t)XCH_GROUP),
-                               (int64_t)grid * SPLIT_P);
+                               (int64_t)grid * split);
             int rc = check_launch("k_zero_i32");
             if (rc) return rc;
         }
         for (int64_t tb = 0; tb == 0 || (seg > 0 && tb < maxlen); tb += (seg > 0 ? seg : INT32_MAX)) {
             const int32_t t0 = (int32_t)tb, t1 = seg > 0 ? (int32_t)std::min<int64_t>(INT32_MAX, tb + seg) : INT32_MAX;
             if (split) {
-                const hipError_t e = launch_decompress_split(m->dev, grid, s, wds, woff, wcnt, len, count, tokens, toff,
-                                                             st, ds, t0, t1, xch, spin_max);
+                const hipError_t e = launch_decompress_split(m->dev, split, grid, s, wds, woff, wcnt, len, count, tokens,
+                                                             toff, st, ds, t0, t1, xch, spin_max);
                 if (e == hipSuccess) {
                     int rc = check_launch("k_decompress (split)");
                     if (rc) return rc;
@@ -1005,7 +1012,7 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
                 // failure is an error)
                 (void)hipGetLastError();
                 if (tb > 0 || e != hipErrorCooperativeLaunchTooLarge) return hip_fail(e, "k_decompress (split)");
-                split = false;
+                split = 0;
             }
             switch (rt) {
 #define SC_DEC_CASE(N)                                                                                        \

@@ -416,39 +416,40 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     __syncthreads();
 }
 
-// Layer 0 of ONE n-tile for one row tile (32 rows), the operands laid out as
-// in gemm_layer0_map, with the weight fragments loaded D k-steps ahead: a
-// wave keeps D fragments (D KB) in flight, as many as a wave of
-// gemm_layer0_map keeps over its four n-tiles.  With one MFMA per k-step the
-// LDS latency has to be hidden as well: a position's four B fragments are
-// read one position ahead, its table address two positions ahead.  The
-// accumulator starts from `init`.  The look-ahead stops at the n-tile's last
-// k-tile.
-template <int D, class AposFn>
-__device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, const uint8_t *s_emb, AposFn apos,
+// Layer 0 of ONE n-tile for one row tile (32 rows) over the NW window
+// positions pf .. pf + NW - 1 (the whole window, or a part when several
+// waves share the n-tile's k-tiles), the operands laid out as in
+// gemm_layer0_map, with the weight fragments loaded D k-steps ahead: a wave
+// keeps D fragments (D KB) in flight, as many as a wave of gemm_layer0_map
+// keeps over its four n-tiles.  With one MFMA per k-step the LDS latency has
+// to be hidden as well: a position's four B fragments are read one position
+// ahead, its table address two positions ahead.  The accumulator starts
+// from `init`.  The look-ahead stops at the range's last k-tile.
+template <int D, int NW, class AposFn>
+__device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, int pf, const uint8_t *s_emb, AposFn apos,
                                                 const v16i &init, int lane) {
     constexpr int KS = EDIM / 32;   // k-steps per position
     constexpr int NP = D / KS;      // positions per loop body
-    static_assert(D % KS == 0 && NP % 2 == 0 && WIN % NP == 0 && WIN / NP >= 2,
-                  "prefetch depth: an even number of positions dividing the window");
+    static_assert(D % KS == 0 && NP % 2 == 0 && NW % NP == 0 && NW / NP >= 2 && NW <= WIN,
+                  "prefetch depth: an even number of positions dividing the range");
     const int voff = nt * KT0 * 1024 + lane * 16;
     v4i w[D];
 #pragma unroll
-    for (int s = 0; s < D; ++s) w[s] = wload(ws, voff, s);
+    for (int s = 0; s < D; ++s) w[s] = wload(ws, voff, pf * KS + s);
     const int rl = lane & 31, kg = (lane >> 5) << 4;
-    // b[x]: the B fragments of the position with parity x; an: the table
-    // address of the next position
+    // b[x]: the B fragments of the position with parity x (relative to pf);
+    // an: the table address of the next position
     v4i b[2][KS];
     {
-        const int e0 = apos(rl, 0) + kg;
+        const int e0 = apos(rl, pf) + kg;
 #pragma unroll
         for (int q = 0; q < KS; ++q) b[0][q] = *(const v4i *)(s_emb + e0 + q * 32);
     }
-    int an = apos(rl, 1);
+    int an = apos(rl, pf + 1);
     v16i acc;
     // D k-steps (NP positions) from position p0; FIRST starts from init,
-    // LAST issues no more weight loads (p0 is a multiple of NP, so position
-    // parity is that of s / KS)
+    // LAST issues no more weight loads (p0 - pf is a multiple of NP, so
+    // relative position parity is that of s / KS)
     auto body = [&](int p0, auto firstc, auto lastc) __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(firstc)::value, LAST = decltype(lastc)::value;
         static_for<D>([&](auto sc) __attribute__((always_inline)) {
@@ -459,22 +460,23 @@ __device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, const
             if constexpr (LAST) wait_counts<D - 1 - s, 15>();
             else wait_counts<D - 1, 15>();
             if constexpr (q == 0) {
-                if (!LAST || p + 1 < WIN) {
+                // (in the last body, position p is the range's s / KS + 1-th from its end)
+                if constexpr (!LAST || s / KS + 1 < NP) {
                     const int e = an + kg;
 #pragma unroll
                     for (int qq = 0; qq < KS; ++qq) b[h ^ 1][qq] = *(const v4i *)(s_emb + e + qq * 32);
                 }
-                if (!LAST || p + 2 < WIN) an = apos(rl, p + 2);
+                if constexpr (!LAST || s / KS + 2 < NP) an = apos(rl, p + 2);
             }
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[s], b[h][q], FIRST && s == 0 ? init : acc, 0, 0, 0);
             if constexpr (!LAST) w[s] = wload(ws, voff, p0 * KS + s + D);
             __builtin_amdgcn_sched_barrier(0);
         });
     };
-    body(0, std::true_type{}, std::false_type{});
+    body(pf, std::true_type{}, std::false_type{});
 #pragma unroll 1
-    for (int p0 = NP; p0 < WIN - NP; p0 += NP) body(p0, std::false_type{}, std::false_type{});
-    body(WIN - NP, std::false_type{}, std::true_type{});
+    for (int p0 = pf + NP; p0 < pf + NW - NP; p0 += NP) body(p0, std::false_type{}, std::false_type{});
+    body(pf + NW - NP, std::false_type{}, std::true_type{});
     return acc;
 }
 

@@ -667,27 +667,34 @@ def _random_chunks(codec, n, hi, seed):
     return tokens, lengths, words, woff, wcnt
 
 
-@pytest.mark.parametrize("n,seg", [(1, None), (3, 64), (33, None), (675, None), (675, 64), (675, 0), (2048, None)])
+@pytest.mark.parametrize("n,seg", [(1, None), (3, 64), (33, None), (675, None), (675, 64), (675, 0), (1024, None),
+                                   (1025, None), (2048, None)])
 def test_split_decode_matches_unsplit(codecs, capfd, monkeypatch, n, seg):
-    """Launches of at most 64 groups of 32 chunks decode split (four
-    workgroups per group share layer 0 and exchange its features every
-    step): one chunk, a partial group, two groups, 22 groups (the c1 case)
-    over 256-step and 64-step segments and one launch, and the largest split
-    launch.  Tokens equal the input and the unsplit decode's
+    """Launches of at most 64 groups of 32 chunks decode split (workgroups
+    of a group share layer 0 and exchange its features every step): eight
+    workgroups per group up to 32 groups, four up to 64 (and four when
+    forced, SC_HIP_DEC_SPLIT=4).  One chunk, a partial group, two groups, 22
+    groups (the c1 case) over 256-step and 64-step segments and one launch,
+    32, 33 and 64 groups.  Tokens equal the input and the unsplit decode's
     (SC_HIP_DEC_SPLIT=0)."""
     codec = codecs["lossless"]
     tokens, lengths, words, woff, wcnt = _random_chunks(codec, n, 700, n)
     _set_dec_env(monkeypatch, seg)
-    capfd.readouterr()
-    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
-    log = capfd.readouterr().err
-    assert "split launch" in log, log
-    assert np.array_equal(back, tokens)
-    monkeypatch.setenv("SC_HIP_DEC_SPLIT", "0")
-    back0, _ = codec.decompress_flat(words, woff, wcnt, lengths)
-    log = capfd.readouterr().err
-    assert "split" not in log and "launch" in log, log
-    assert np.array_equal(back0, tokens)
+    groups = (n + 31) // 32
+    modes = [(None, "split launch p8" if groups <= 32 else "split launch p4")]
+    if groups <= 32:
+        modes.append(("4", "split launch p4"))
+    modes.append(("0", "launch"))
+    for env, expect in modes:
+        if env is None:
+            monkeypatch.delenv("SC_HIP_DEC_SPLIT", raising=False)
+        else:
+            monkeypatch.setenv("SC_HIP_DEC_SPLIT", env)
+        capfd.readouterr()
+        back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+        log = capfd.readouterr().err
+        assert f"leftover {n} {expect} steps" in log, log
+        assert np.array_equal(back, tokens), env
 
 
 def test_split_decode_not_used_beyond_64_groups(codecs, capfd, monkeypatch):
