@@ -182,6 +182,29 @@ def roofline(kernel, tokens, seconds, config, direction):
             **ceiling_fields(achieved), **pmc_mfma(config, kernel)}
 
 
+PEAK_L1_GBS_PER_CU = 64 * 2.4   # vector L1 fill: 64 bytes per clock at the 2.4 GHz peak engine clock
+
+
+def split_roofline(model, lengths, seconds, n_cu):
+    """Bound of a decode that runs split (fewer than 32 x n_cu chunks in at
+    most 64 groups of 32 that the CUs hold with 4 or 8 workgroups each, as
+    sc_decompress_chunks plans it): each active CU streams its share of
+    layer 0 plus every later layer's weights through its vector L1 once per
+    step.  None when the decode does not run split."""
+    n = len(lengths)
+    groups = -(-n // 32)
+    if n >= 32 * n_cu or groups > 64 or groups * 4 > n_cu:
+        return None
+    p = 8 if groups * 8 <= n_cu else 4
+    per_cu = model.layers[0].n * model.layers[0].k // p + sum(L.n * L.k for L in model.layers[1:])
+    steps = int(lengths.max())
+    gbs = per_cu * steps / seconds / 1e9
+    return {"kernel": f"k_decompress (split, {p} workgroups per 32-chunk group)", "bound": "vector L1 fill per CU",
+            "achieved": round(gbs, 2), "peak": PEAK_L1_GBS_PER_CU, "unit": "GB/s per CU",
+            "frac": round(gbs / PEAK_L1_GBS_PER_CU, 4),
+            "algorithmic": f"{per_cu} weight bytes per CU per step x {steps} steps, {groups * p} CUs active"}
+
+
 def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
     """One configuration's GPU compress + decompress, timed with HIP events on
     its own stream; every chunk round-trips, 24 random chunks' bytes are
@@ -285,6 +308,9 @@ def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
         "roofline": roofline("k_decompress", n_tokens, t_d, name, "decoded"),
         "roofline_compress": roofline("k_compress_mlp", n_tokens, t_c, name, "coded"),
     }
+    rl1 = split_roofline(codec.model, lengths, t_d, torch.cuda.get_device_properties(0).multi_processor_count)
+    if rl1:
+        res["roofline_split"] = rl1
     if e2e:
         # the first pass also allocates the pinned staging buffers (torch keeps
         # them cached): report the second, as a process that compresses
