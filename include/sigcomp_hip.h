@@ -236,8 +236,8 @@ int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
  * same rows.  A launch of at most 64 groups of 32 chunks runs split: 8
  * workgroups per group (4 when the CUs cannot hold 8) share layer 0 and
  * wait for each other every step (a cooperative launch, so all are
- * resident; a bounded wait, SC_STATUS_SYNC_TIMEOUT when it expires).
- * Replaces
+ * resident; a bounded wait, SC_STATUS_SYNC_TIMEOUT when it expires), except
+ * on a stream under graph capture.  Replaces
  * QuantMLPCompression.decompress_chunks / _decompress_chunks_gpu
  * (quant_mlp_export.py:325-377); output equals
  * CPUQuantMLPCompression.decompress_chunks (cpu_compression.py:259-332). */

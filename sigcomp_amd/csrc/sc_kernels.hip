@@ -939,7 +939,12 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
     // that split, for comparisons)
     const char *split_env = getenv("SC_HIP_DEC_SPLIT");
     const int split_force = split_env ? atoi(split_env) : -1;
-    const bool split_ok = m->dev.pipe == CORE_PIPE_UNI && xch && split_force != 0;
+    // (a stream under graph capture gets the unsplit launches: the split
+    // one is a cooperative launch)
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    SC_HIP(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+    const bool split_ok =
+        m->dev.pipe == CORE_PIPE_UNI && xch && split_force != 0 && capture == hipStreamCaptureStatusNone;
     // polls before a wait for the peers gives up (SC_HIP_DEC_SPIN: a lower
     // limit, to test the timeout path)
     const char *spin_env = getenv("SC_HIP_DEC_SPIN");

@@ -89,3 +89,44 @@ def test_static_entry_rejects_more_chunks_than_its_array(codec):
     rc = L.sc_decompress_chunks_static(codec.hip.handle, p, p, p, p, n, p, p, p, None,
                                        torch.cuda.current_stream().cuda_stream)
     assert rc != 0 and b"at most" in L.sc_last_error()
+
+
+def test_static_entry_under_graph_capture(codec):
+    """The entry point's callers include code under HIP graph capture: 40
+    chunks over two 256-step segments (a batch that decodes split when not
+    captured; a capturing stream gets the unsplit launches) captured once
+    and replayed three times, with eager work between the replays that
+    overwrites the outputs; every replay equals the eager decode and the
+    input."""
+    from sigcomp_amd import _hip
+    L = _hip.lib()
+    tokens, lengths, words, woff, wcnt = _inputs(codec, 40, 300, 600, 5)
+    ref_tok, ref_st = _decode(codec, "static", words, woff, wcnt, lengths, True)
+    assert not ref_st.any()
+    src = np.concatenate([[0], np.cumsum(lengths[:-1])]).astype(np.int64)
+    assert np.array_equal(ref_tok, np.concatenate([tokens[src[c]:src[c] + lengths[c]] for c in range(40)]))
+    n = len(lengths)
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_words, t_woff, t_cnt = d(words.view(np.int32)), d(woff.astype(np.int64)), d(wcnt.astype(np.int32))
+    t_len, t_toff = d(lengths.astype(np.int32)), d(tok_off)
+    out = torch.empty(int(lengths.sum()), dtype=torch.uint8, device="cuda")
+    status = torch.empty(n, dtype=torch.int32, device="cuda")
+    len_host = np.ascontiguousarray(lengths, np.int32)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        _hip.check(L.sc_decompress_chunks_static(
+            codec.hip.handle, t_words.data_ptr(), t_woff.data_ptr(), t_cnt.data_ptr(), t_len.data_ptr(), n,
+            out.data_ptr(), t_toff.data_ptr(), status.data_ptr(), len_host.ctypes.data,
+            torch.cuda.current_stream().cuda_stream))
+    for rep in range(3):
+        out.fill_(0xAB)
+        status.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(status.cpu().numpy(), ref_st), rep
+        assert np.array_equal(out.cpu().numpy(), ref_tok), rep
