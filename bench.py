@@ -501,22 +501,10 @@ def cpu_full(raw, hw):
 
 # ----------------------------------------------------------------- c2
 
-def run_mlp(rows, steps, warmup, sampler):
-    """Config c2: `rows` context rows -> int32 CDF tables, seeded random
-    per-channel model with the bundled checkpoints' layer dims; 256 random
-    rows checked against the oracle."""
+def _time_mlp(hm, ctx_d, steps, warmup, sampler):
+    """HIP-event time per forward_windows(ctx, "cdf") launch and the power
+    window of the timed launches -> (seconds, power dict or None, output)."""
     import torch
-    from sigcomp_amd import signal, synth
-    from sigcomp_amd.model_io import random_int_model
-    from sigcomp_amd.quant_mlp_export import HipModel
-    m = random_int_model(seed=2, per_channel=True)
-    hm = HipModel(m, torch.device("cuda:0"))
-    toks = np.concatenate([signal.split_signal(r)[1] for r in synth.synth_reads(64, 202, synth.DNA)])
-    toks = toks.astype(np.int64)
-    starts = np.random.default_rng(3).integers(-63, len(toks) - 64, rows)
-    idx = starts[:, None] + np.arange(64)[None, :]
-    ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
-    ctx_d = torch.from_numpy(ctx).cuda()
     for _ in range(warmup):
         hm.forward_windows(ctx_d, "cdf")
     torch.cuda.synchronize()
@@ -528,16 +516,51 @@ def run_mlp(rows, steps, warmup, sampler):
     e1.record()
     torch.cuda.synchronize()
     t1 = time.monotonic()
-    t = e0.elapsed_time(e1) / 1e3 / steps
+    return e0.elapsed_time(e1) / 1e3 / steps, (sampler.window(t0, t1) if sampler else None), out
+
+
+def run_mlp(rows, steps, warmup, sampler):
+    """Config c2: `rows` context rows -> int32 CDF tables, seeded random
+    per-channel model with the bundled checkpoints' layer dims; 256 random
+    rows checked against the oracle.  Beside it, the same rows through the
+    same kernel with a random per-tensor model and with the bundled lossless
+    checkpoint (what per-channel constants and uniform random weights cost;
+    each checked on 64 rows)."""
+    import torch
+    from sigcomp_amd import signal, synth
+    from sigcomp_amd.model_io import DEFAULT_QUANT_LOSSLESS_MODEL_PATH, load_int_model, random_int_model
+    from sigcomp_amd.quant_mlp_export import HipModel
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
-    sub = np.random.default_rng(4).choice(rows, 256, replace=False)
-    om = oracle.OracleModel(m)
-    ref = oracle.logits_to_cdf(oracle.mlp_forward(om, ctx[sub]), m.exp_lut)
-    if not np.array_equal(out[torch.from_numpy(sub).cuda()].cpu().numpy().astype(np.int64), ref):
-        raise RuntimeError("c2 CDF mismatch vs oracle")
+    m = random_int_model(seed=2, per_channel=True)
+    hm = HipModel(m, torch.device("cuda:0"))
+    toks = np.concatenate([signal.split_signal(r)[1] for r in synth.synth_reads(64, 202, synth.DNA)])
+    toks = toks.astype(np.int64)
+    starts = np.random.default_rng(3).integers(-63, len(toks) - 64, rows)
+    idx = starts[:, None] + np.arange(64)[None, :]
+    ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
+    ctx_d = torch.from_numpy(ctx).cuda()
+
+    def check(model, out, n, seed):
+        sub = np.random.default_rng(seed).choice(rows, n, replace=False)
+        ref = oracle.logits_to_cdf(oracle.mlp_forward(oracle.OracleModel(model), ctx[sub]), model.exp_lut)
+        if not np.array_equal(out[torch.from_numpy(sub).cuda()].cpu().numpy().astype(np.int64), ref):
+            raise RuntimeError("c2 CDF mismatch vs oracle")
+
+    t, pw, out = _time_mlp(hm, ctx_d, steps, warmup, sampler)
+    check(m, out, 256, 4)
     achieved = rows * OPS_PER_ROW / t / 1e12
-    pw = sampler.window(t0, t1) if sampler else None
+    side = {}
+    for name, model in (("random_per_tensor", random_int_model(seed=2, per_channel=False)),
+                        ("lossless_checkpoint", load_int_model(DEFAULT_QUANT_LOSSLESS_MODEL_PATH))):
+        h2 = HipModel(model, torch.device("cuda:0"))
+        t2, pw2, out2 = _time_mlp(h2, ctx_d, min(steps, 200), warmup, sampler)
+        check(model, out2, 64, 5)
+        side[name] = {"mrows_s": round(rows / t2 / 1e6, 3), "achieved_tops": round(rows * OPS_PER_ROW / t2 / 1e12, 2),
+                      "core": h2.core, "mean_abs_weight": round(float(np.mean(
+                          [np.abs(L.weight.astype(np.int32)).mean() for L in model.layers])), 2),
+                      "avg_w": pw2["avg_w"] if pw2 else None}
+        del h2, out2
     return {"workload": f"c2: {rows} context rows -> int32 CDF tables, random per-channel int8 model with the "
                         "checkpoints' layer dims",
             "mrows_s": round(rows / t / 1e6, 3), "ms_per_step": round(t * 1e3, 3), "steps": steps,
@@ -547,7 +570,9 @@ def run_mlp(rows, steps, warmup, sampler):
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
                          "traffic": None,
                          "algorithmic": f"{OPS_PER_ROW} int8 ops per row x {rows} rows per launch",
-                         **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")}}
+                         **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")},
+            "same_rows_other_models": {**side, "note": "the same rows and kernel with a random per-tensor model "
+                                                       "and with the bundled lossless checkpoint; not the c2 figure"}}
 
 
 def bench_mlp(args):
@@ -555,7 +580,8 @@ def bench_mlp(args):
     return {"metric": "INT8 MLP rows/s -> int32 CDF (c2 microbench)", "value": r["mrows_s"], "unit": "Mrows/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-            "data": "synthetic", "config": {"workload": r["workload"]}, "roofline": r["roofline"]}
+            "data": "synthetic", "config": {"workload": r["workload"]}, "roofline": r["roofline"],
+            "same_rows_other_models": r["same_rows_other_models"]}
 
 
 # ------------------------------------------------------- ceiling, coder
