@@ -315,15 +315,29 @@ __device__ __forceinline__ void split_params_init(const ModelDev &M, uint32_t *s
     if (lane < Slot<true>::TD) blk[lane] = M.layer[0].par[nt * PAR_DWORDS + lane];
 }
 
+// Layer 0 carried from one step of the split decode to the next: the wave's
+// sums over every window position but the last (whose token the step
+// decodes), and the last position's weight fragments.
+struct L0Carry {
+    v16i acc;
+    v4i wlast[EDIM / 32];
+    bool have;
+};
+
 // One MLP evaluation of the group's 32 rows, layer 0 shared (above).  Same
 // contract as mlp_rows_pipe<1, true>; `xbuf` / `flags` are the group's
 // exchange buffers and step flags, s_err the workgroup's timeout flag,
-// s_red (P = 8) 2 x 4 KB of LDS for the partial sums.
-template <int P, class AposFn>
+// s_red (P = 8) 2 x 4 KB of LDS for the partial sums.  Once a step has
+// published its features it streams the next step's layer 0 but the last
+// position (apos_next, when has_next) into `l0`, so that the next step
+// starts with four MFMAs while this step's exchange completes behind that
+// work; the first step of a launch computes the whole window.
+template <int P, class AposFn, class AposNextFn>
 __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t *s_emb, uint8_t *s_act,
-                                               uint32_t *s_par, AposFn apos, int wave, int lane, uint8_t *xbuf,
-                                               int32_t *flags, int slice, int32_t t, int32_t spin_max,
-                                               int32_t *s_err, int32_t *s_red) {
+                                               uint32_t *s_par, AposFn apos, AposNextFn apos_next, bool has_next,
+                                               L0Carry &l0, int wave, int lane, uint8_t *xbuf, int32_t *flags,
+                                               int slice, int32_t t, int32_t spin_max, int32_t *s_err,
+                                               int32_t *s_red) {
     static_assert(P == 4 || P == 8, "one or two layer-0 n-tiles per wave pair");
     constexpr int NTW = 16 / P;           // layer-0 n-tiles of the workgroup
     constexpr int KSPLIT = WAVES / NTW;   // waves per n-tile, each over WIN / KSPLIT positions
@@ -342,15 +356,20 @@ __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t 
     const LayerDev &L0 = M.layer[0];
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *)(xbuf + (t & 1) * XCH_PAR), (short)0, XCH_PAR, 0x00020000);
+    const int nt = split_ntile<P>(slice, wave), kp = wave / NTW;   // n-tile, part of the window
+    const bool lastpart = kp == KSPLIT - 1;                          // the part holding the last position
+    constexpr int NW = WIN / KSPLIT;
+    const WStream ws0 = make_wstream(L0.w, L0.bytes);
+    const v16i bias = bias_tile<UNI>(s_parw + slot_p0(0) * BLK, 0, g2);
+    const v16i zero = {};
     {
-        const int nt = split_ntile<P>(slice, wave), kp = wave / NTW;   // n-tile, part of the window
         uint32_t prn[Slot<UNI>::LANE];
         par_fetch<UNI>(M.layer[1].par, nb0, lane, prn);
-        const v16i bias = bias_tile<UNI>(s_parw + slot_p0(0) * BLK, 0, g2);
-        const v16i zero = {};
-        constexpr int NW = WIN / KSPLIT;
-        v16i a0[1] = {gemm_layer0_one<L0_DEPTH, NW>(make_wstream(L0.w, L0.bytes), nt, kp * NW, s_emb, apos,
-                                                    kp == 0 ? bias : zero, lane)};
+        v16i a0[1];
+        if (l0.have)
+            a0[0] = lastpart ? gemm_layer0_position(l0.wlast, WIN - 1, s_emb, apos, l0.acc, lane) : l0.acc;
+        else
+            a0[0] = gemm_layer0_one<L0_DEPTH, NW>(ws0, nt, kp * NW, s_emb, apos, kp == 0 ? bias : zero, lane);
         par_put<UNI>(s_parw + slot_p0(1) * BLK, prn, lane);
         if constexpr (KSPLIT > 1) {
             // the second half's partial sums -> the first half's wave
@@ -383,6 +402,11 @@ __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t 
     __syncthreads();
     const bool err = *s_err != 0;
     if (threadIdx.x == 0 && !err) __hip_atomic_store(flags + slice, t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the next step's layer 0 but its last position while the features travel
+    l0.have = has_next;
+    if (has_next)
+        l0.acc = gemm_layer0_one<L0_DEPTH, NW>(ws0, nt, kp * NW, s_emb, apos_next, kp == 0 ? bias : zero, lane,
+                                               lastpart, l0.wlast);
     // the first hidden layer's first weight fragments while the peers finish
     {
         const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
@@ -584,17 +608,24 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         }
         __syncthreads();
     }
+    L0Carry l0c;   // (split decode) layer 0 carried between steps
+    l0c.have = false;
     for (int32_t t = t_begin; t < t_stop; ++t) {
         auto apos = [&](int r, int p) {
             if (t + p < WIN) return emb_off(SOS, 0);
             if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
             else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
         };
-        if constexpr (P > 1)
-            mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, wave, lane, xch + group * XCH_GROUP,
-                              (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P, slice, t,
-                              spin_max, &s_xerr, s_red);
-        else
+        if constexpr (P > 1) {
+            // the next step's window, of which all but the last position is known
+            auto apos_next = [&](int r, int p) {
+                if (t + 1 + p < WIN) return emb_off(SOS, 0);
+                return (int)s_apos[apos_at(r, t + 1 + p)];
+            };
+            mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, apos_next, t + 1 < t_stop, l0c, wave, lane,
+                              xch + group * XCH_GROUP, (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P,
+                              slice, t, spin_max, &s_xerr, s_red);
+        } else
             mlp_tile<CORE, RT>(M, s_emb, s_act, s_par, apos, wave, lane);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
         // _decode_partition (cpu_entropy_coding.py:230-266): every lane of a

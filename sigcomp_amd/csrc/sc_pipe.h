@@ -424,10 +424,14 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
 // keeps over its four n-tiles.  With one MFMA per k-step the LDS latency has
 // to be hidden as well: a position's four B fragments are read one position
 // ahead, its table address two positions ahead.  The accumulator starts
-// from `init`.  The look-ahead stops at the range's last k-tile.
+// from `init`.  The look-ahead stops at the range's last k-tile.  With
+// `skip_last` (wave-uniform) the range's last position is loaded but not
+// multiplied: its fragments are left in `wlast` for gemm_layer0_position
+// once its token is known.
 template <int D, int NW, class AposFn>
 __device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, int pf, const uint8_t *s_emb, AposFn apos,
-                                                const v16i &init, int lane) {
+                                                const v16i &init, int lane, bool skip_last = false,
+                                                v4i *wlast = nullptr) {
     constexpr int KS = EDIM / 32;   // k-steps per position
     constexpr int NP = D / KS;      // positions per loop body
     static_assert(D % KS == 0 && NP % 2 == 0 && NW % NP == 0 && NW / NP >= 2 && NW <= WIN,
@@ -468,7 +472,13 @@ __device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, int p
                 }
                 if constexpr (!LAST || s / KS + 2 < NP) an = apos(rl, p + 2);
             }
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[s], b[h][q], FIRST && s == 0 ? init : acc, 0, 0, 0);
+            if constexpr (LAST && s / KS == NP - 1) {
+                // the range's last position
+                if (skip_last) wlast[q] = w[s];
+                else acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[s], b[h][q], acc, 0, 0, 0);
+            } else {
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[s], b[h][q], FIRST && s == 0 ? init : acc, 0, 0, 0);
+            }
             if constexpr (!LAST) w[s] = wload(ws, voff, p0 * KS + s + D);
             __builtin_amdgcn_sched_barrier(0);
         });
@@ -477,6 +487,21 @@ __device__ __forceinline__ v16i gemm_layer0_one(const WStream &ws, int nt, int p
 #pragma unroll 1
     for (int p0 = pf + NP; p0 < pf + NW - NP; p0 += NP) body(p0, std::false_type{}, std::false_type{});
     body(pf + NW - NP, std::false_type{}, std::true_type{});
+    return acc;
+}
+
+// Position p of layer 0 for one n-tile and row tile, its weight fragments
+// already in registers (gemm_layer0_one's `wlast`): acc + W_p . emb(tok(r, p)).
+template <class AposFn>
+__device__ __forceinline__ v16i gemm_layer0_position(const v4i *wp, int p, const uint8_t *s_emb, AposFn apos,
+                                                     v16i acc, int lane) {
+    constexpr int KS = EDIM / 32;
+    const int e = apos(lane & 31, p) + ((lane >> 5) << 4);
+    v4i b[KS];
+#pragma unroll
+    for (int q = 0; q < KS; ++q) b[q] = *(const v4i *)(s_emb + e + q * 32);
+#pragma unroll
+    for (int q = 0; q < KS; ++q) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wp[q], b[q], acc, 0, 0, 0);
     return acc;
 }
 
