@@ -176,25 +176,48 @@ __device__ __forceinline__ v4i global_logits16(const int8_t *logits, int64_t row
     return row < rows ? *(const v4i *)(logits + row * VOCAB + 16 * u) : v4i{0, 0, 0, 0};
 }
 
+// Each wave's 4 rows (4 x 257 int64, one contiguous span of the output)
+// are staged in LDS and written out as 16-byte pieces by consecutive lanes:
+// written straight from the lanes, each store instruction would scatter 64
+// 8-byte pieces 128 bytes apart.  LDS rows hold one pad slot per 16 values,
+// so that the 16 lanes of a row (16 values apart) write different banks.
+constexpr int CDF_LDS_ROW = VOCAB + 1 + 17;   // 257 values + 16 pads, even
+__device__ __forceinline__ int cdf_lds_at(int v) { return v + (v >> 4); }
+
 __global__ __launch_bounds__(256) void k_logits_to_cdf(const int8_t *__restrict__ logits, int64_t rows,
                                                        const uint64_t *__restrict__ lut,
                                                        int64_t *__restrict__ cdf) {
     __shared__ double s_lut[VOCAB];
-    const int u = threadIdx.x & 15;
+    __shared__ __attribute__((aligned(16))) int64_t s_out[WAVES][4 * CDF_LDS_ROW];
+    const int u = threadIdx.x & 15, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const v4i raw = global_logits16(logits, r, rows, u);
     stage_lut(lut, s_lut);
     Freq16 fr;
     row_frequencies16(raw, s_lut, u, fr);
-    if (r >= rows) return;
-    int64_t *dst = cdf + r * (VOCAB + 1) + 16 * u;
+    int64_t *so = s_out[wave] + (lane >> 4) * CDF_LDS_ROW;
     uint32_t c = fr.ex;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        dst[k] = c;
+        so[cdf_lds_at(16 * u + k)] = c;
         c += fr.f[k];
     }
-    if (u == 15) dst[16] = TOTAL;
+    if (u == 15) so[cdf_lds_at(VOCAB)] = TOTAL;
+    // the wave's own LDS writes before its reads (LDS runs a wave's accesses in order)
+    slot_sync();
+    const int64_t r0 = (int64_t)blockIdx.x * 16 + wave * 4;
+    if (r0 >= rows) return;
+    const int n = (int)min<int64_t>(4, rows - r0) * (VOCAB + 1);   // values of the span
+    int64_t *dst = cdf + r0 * (VOCAB + 1);   // 16-byte aligned: r0 is a multiple of 4, 4 x 2056 = 8224 bytes
+    const int64_t *sw = s_out[wave];
+    auto at = [&](int i) { return sw[(i / (VOCAB + 1)) * CDF_LDS_ROW + cdf_lds_at(i % (VOCAB + 1))]; };
+    for (int i = 2 * lane; i < n; i += 128) {
+        if (i + 1 < n) {
+            *(longlong2 *)(dst + i) = make_longlong2(at(i), at(i + 1));
+        } else {
+            dst[i] = at(i);
+        }
+    }
 }
 
 struct EncArrays {
