@@ -97,6 +97,13 @@ int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *d
                   uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,
                   int64_t *bad);
 
+/* sc_host_parse with each read's payload at its own address, payload[r]
+ * (data_len[r] bytes): the caller's per-read buffers (the reference's list
+ * of bytes objects) are parsed where they are, without first joining them. */
+int sc_host_parse_v(const uint8_t *const *payload, const int64_t *data_len, const int64_t *tokens, int64_t n_reads,
+                    int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off, uint32_t *words_out,
+                    int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads, int64_t *bad);
+
 /* ------------------------------------------------------------ SIG2 records
  *
  * A SIG2 archive is MAGIC 'SIG2', a uint32 length and the header blob (the

@@ -25,7 +25,7 @@ ERR_POSITION = 15
 ERR_EMPTY_READ = 16
 
 EXPORTED = ("sc_host_last_error", "sc_host_split_count", "sc_host_split_fill", "sc_host_reassemble",
-            "sc_host_frame", "sc_host_parse")
+            "sc_host_frame", "sc_host_parse", "sc_host_parse_v")
 
 # the exception type the reference raises for each failure
 _MESSAGES = {
@@ -62,6 +62,7 @@ def lib():
         L.sc_host_reassemble.argtypes = [_P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P]
         L.sc_host_frame.argtypes = [_P, _P, _P, _I64, _P, _P, _I32, _P]
         L.sc_host_parse.argtypes = [_P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I32, _P]
+        L.sc_host_parse_v.argtypes = [_P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I32, _P]
         for name in EXPORTED[1:]:
             getattr(L, name).restype = ctypes.c_int
         _LIB = L
@@ -183,8 +184,18 @@ def parse(payloads, tokens, chunk_len: int, n_threads: int = 0, words_out=None) 
     if len(tokens) != n:
         raise ValueError("Compressed read and token length counts differ")
     data_len = np.fromiter((len(p) for p in payloads), np.int64, count=n)
-    data_off = _excl_scan(data_len)
-    data = np.frombuffer(b"".join(payloads), np.uint8) if n else np.zeros(0, np.uint8)
+    # each payload's own buffer, no joined copy: bytes objects through
+    # c_char_p (their internal buffer), anything else as a uint8 view
+    views = []
+
+    def addr(p):
+        if type(p) is bytes:
+            return ctypes.cast(ctypes.c_char_p(p), ctypes.c_void_p).value or 0
+        a = np.frombuffer(p, np.uint8)
+        views.append(a)
+        return a.ctypes.data
+
+    payload_ptr = np.fromiter((addr(p) for p in payloads), np.uint64, count=n) if n else np.zeros(1, np.uint64)
     frames = (tokens + chunk_len - 1) // chunk_len
     chunk_begin = _excl_scan(frames)
     n_chunks = int(frames.sum())
@@ -201,8 +212,9 @@ def parse(payloads, tokens, chunk_len: int, n_threads: int = 0, words_out=None) 
     word_cnt = np.zeros(n_chunks, np.int32)
     tok_cnt = np.zeros(n_chunks, np.int32)
     bad = ctypes.c_int64(-1)
-    _check(lib().sc_host_parse(_p(data), _p(data_off), _p(data_len), _p(tokens), n, int(chunk_len),
-                               _p(chunk_begin), _p(read_word_off), _p(words), _p(word_off), _p(word_cnt),
-                               _p(tok_cnt), int(n_threads), ctypes.byref(bad)), bad, "read")
+    _check(lib().sc_host_parse_v(_p(payload_ptr), _p(data_len), _p(tokens), n, int(chunk_len),
+                                 _p(chunk_begin), _p(read_word_off), _p(words), _p(word_off), _p(word_cnt),
+                                 _p(tok_cnt), int(n_threads), ctypes.byref(bad)), bad, "read")
+    del views, payload_ptr   # (the payloads themselves are the caller's)
     return {"words": words, "word_off": word_off, "word_cnt": word_cnt, "tok_cnt": tok_cnt,
             "chunk_begin": chunk_begin, "frames": frames}

@@ -105,6 +105,52 @@ inline int16_t unzigzag(uint16_t z) {
 
 }  // namespace
 
+namespace {
+
+// Parse of framed reads (sc_host_parse): `payload(r)` is read r's data.
+template <class PayloadFn>
+int parse_reads(PayloadFn payload, const int64_t *data_len, const int64_t *tokens, int64_t n_reads, int32_t chunk_len,
+                const int64_t *chunk_begin, const int64_t *read_word_off, uint32_t *words_out, int64_t *word_off,
+                int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads, int64_t *bad) {
+    if (n_reads < 0 || chunk_len < 1 ||
+        (n_reads && (!data_len || !tokens || !chunk_begin || !read_word_off || !word_off || !word_cnt ||
+                     !tok_cnt))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    parallel_for(n_reads, n_threads, [&](int64_t r) {
+        const uint8_t *d = payload(r);
+        const int64_t size = data_len[r];
+        int64_t remaining = tokens[r], pos = 0, c = chunk_begin[r], w = read_word_off[r];
+        while (remaining > 0) {
+            if (pos + 2 > size) {
+                fb.report(r, SC_HOST_ERR_FRAME_LENGTH);
+                return;
+            }
+            const int64_t fbytes = (int64_t)d[pos] | ((int64_t)d[pos + 1] << 8);
+            pos += 2;
+            if (fbytes == 0 || fbytes % 4 || pos + fbytes > size) {
+                fb.report(r, SC_HOST_ERR_FRAME);
+                return;
+            }
+            const int64_t count = std::min<int64_t>(chunk_len, remaining);
+            std::memcpy(words_out + w, d + pos, (size_t)fbytes);
+            word_off[c] = w;
+            word_cnt[c] = (int32_t)(fbytes / 4);
+            tok_cnt[c] = (int32_t)count;
+            w += fbytes / 4;
+            pos += fbytes;
+            remaining -= count;
+            ++c;
+        }
+        if (pos != size) fb.report(r, SC_HOST_ERR_TRAILING);
+    });
+    return finish(fb, bad);
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *sc_host_last_error(void) { return g_err.c_str(); }
@@ -255,41 +301,23 @@ int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *d
                   int64_t n_reads, int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off,
                   uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,
                   int64_t *bad) {
-    if (n_reads < 0 || chunk_len < 1 ||
-        (n_reads && (!data_off || !data_len || !tokens || !chunk_begin || !read_word_off || !word_off ||
-                     !word_cnt || !tok_cnt))) {
+    if (n_reads && !data_off) {
         g_err = "bad argument";
         return SC_ERR_ARG;
     }
-    FirstBad fb;
-    parallel_for(n_reads, n_threads, [&](int64_t r) {
-        const uint8_t *d = data + data_off[r];
-        const int64_t size = data_len[r];
-        int64_t remaining = tokens[r], pos = 0, c = chunk_begin[r], w = read_word_off[r];
-        while (remaining > 0) {
-            if (pos + 2 > size) {
-                fb.report(r, SC_HOST_ERR_FRAME_LENGTH);
-                return;
-            }
-            const int64_t fbytes = (int64_t)d[pos] | ((int64_t)d[pos + 1] << 8);
-            pos += 2;
-            if (fbytes == 0 || fbytes % 4 || pos + fbytes > size) {
-                fb.report(r, SC_HOST_ERR_FRAME);
-                return;
-            }
-            const int64_t count = std::min<int64_t>(chunk_len, remaining);
-            std::memcpy(words_out + w, d + pos, (size_t)fbytes);
-            word_off[c] = w;
-            word_cnt[c] = (int32_t)(fbytes / 4);
-            tok_cnt[c] = (int32_t)count;
-            w += fbytes / 4;
-            pos += fbytes;
-            remaining -= count;
-            ++c;
-        }
-        if (pos != size) fb.report(r, SC_HOST_ERR_TRAILING);
-    });
-    return finish(fb, bad);
+    return parse_reads([&](int64_t r) { return data + data_off[r]; }, data_len, tokens, n_reads, chunk_len,
+                       chunk_begin, read_word_off, words_out, word_off, word_cnt, tok_cnt, n_threads, bad);
+}
+
+int sc_host_parse_v(const uint8_t *const *payload, const int64_t *data_len, const int64_t *tokens, int64_t n_reads,
+                    int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off, uint32_t *words_out,
+                    int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads, int64_t *bad) {
+    if (n_reads && !payload) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    return parse_reads([&](int64_t r) { return payload[r]; }, data_len, tokens, n_reads, chunk_len, chunk_begin,
+                       read_word_off, words_out, word_off, word_cnt, tok_cnt, n_threads, bad);
 }
 
 }  // extern "C"

@@ -163,6 +163,43 @@ def test_parse_matches_python_parse_and_errors():
         assert "read 1" in str(host_err.value)
 
 
+def test_parse_reads_payloads_in_place_from_any_buffer():
+    """parse takes each payload where it lies (sc_host_parse_v, no joined
+    copy): bytes, bytearray, memoryview and numpy payloads in one call give
+    the words of sc_host_parse over the joined data, and the payloads are
+    left as they were."""
+    import ctypes
+    _host = _lib_or_skip()
+    rng = np.random.default_rng(9)
+    tokens = [0, 5, 8, 17, 40, 3]
+    payloads = [_payload(rng, t, 8) for t in tokens]
+    mixed = [payloads[0], bytearray(payloads[1]), memoryview(payloads[2]),
+             np.frombuffer(payloads[3], np.uint8).copy(), payloads[4], bytes(payloads[5])]
+    before = [bytes(p) for p in mixed]
+    pr = _host.parse(mixed, tokens, 8)
+    assert [bytes(p) for p in mixed] == before
+    # the joined-buffer entry point on the same data
+    L = _host.lib()
+    data = np.frombuffer(b"".join(payloads), np.uint8)
+    lens = np.array([len(p) for p in payloads], np.int64)
+    off = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    tk = np.array(tokens, np.int64)
+    frames = (tk + 7) // 8
+    cb = np.concatenate([[0], np.cumsum(frames)[:-1]]).astype(np.int64)
+    rwo = np.concatenate([[0], np.cumsum(lens // 4)[:-1]]).astype(np.int64)
+    nc = int(frames.sum())
+    words = np.zeros(max(int((lens // 4).sum()), 1), np.uint32)
+    wo, wc, tc = np.zeros(nc, np.int64), np.zeros(nc, np.int32), np.zeros(nc, np.int32)
+    bad = ctypes.c_int64(-1)
+    p = lambda a: a.ctypes.data
+    assert L.sc_host_parse(p(data), p(off), p(lens), p(tk), len(tokens), 8, p(cb), p(rwo), p(words), p(wo), p(wc),
+                           p(tc), 0, ctypes.byref(bad)) == 0
+    assert np.array_equal(pr["word_off"], wo) and np.array_equal(pr["word_cnt"], wc)
+    for c in range(nc):   # the words each chunk wrote (a read's slots past its frames are not written)
+        assert np.array_equal(pr["words"][wo[c]:wo[c] + wc[c]], words[wo[c]:wo[c] + wc[c]])
+    assert np.array_equal(pr["tok_cnt"], tc)
+
+
 class _OracleCodec:
     """CPU codec around the C oracle with the GPU codec's flat interface, so
     that the batched framing path of ReadFramingMixin runs here."""
