@@ -338,6 +338,11 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     static_for<NV>([&](auto vc) __attribute__((always_inline)) {
         constexpr int v = decltype(vc)::value;
         constexpr int pass = v / KTH, kt = v % KTH, set = (v / PPD) & 1, slot = v % PPD;
+        // one wait per k-step for its weight fragments (issued PPD steps
+        // ago; the 2 * LANE parameter loads at the top of this function
+        // are younger than the first PPD steps' fragments) and its B
+        // fragments, instead of the compiler's wait before each first use
+        wait_counts<(PPD - 1) * PNT + (v < PPD && !LASTL ? 2 * Slot<UNI>::LANE : 0), 0>();
         // next step's B fragments (none across a barrier)
         if constexpr (v != 7 && v != NV - 1) read_b<RT>(s_act, bbase, (kt + 1) % KTH, b[(kt + 1) & 1]);
         // weights PPD steps ahead: this layer, else the next layer's pass 0
