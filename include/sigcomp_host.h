@@ -126,6 +126,8 @@ int sc_host_parse_v(const uint8_t *const *payload, const int64_t *data_len, cons
 #define SC_HOST_ERR_BAD_COUNTS  21  /* N < 1 or small tokens > N - 1 [ValueError] */
 #define SC_HOST_ERR_TRAILING_RECORDS 22  /* bytes after the last record [ValueError] */
 #define SC_HOST_ERR_INDEX       23  /* bad magic / count / size / offset [ValueError] */
+#define SC_HOST_ERR_RICE        24  /* invalid, truncated or trailing Rice blob [ValueError] */
+#define SC_HOST_ERR_RICE_RANGE  25  /* value does not fit the fallback width [ValueError] */
 
 /* REC_FMT fields in order (main.py:905-917). */
 typedef struct {
@@ -174,6 +176,45 @@ int sc_sig2_write_index(int64_t n, const uint8_t *read_ids, const uint64_t *offs
  * and offsets.  *bad = the offending entry (-1 for the header). */
 int sc_sig2_read_index(const uint8_t *data, int64_t size, int64_t n_expected, int64_t data_start,
                        int64_t file_size, uint8_t *read_ids, uint64_t *offsets, int64_t *bad);
+
+/* ---- Rice coding of the large values and their gap-coded positions ------
+ *
+ * Replaces fast_rice.rice_encode / rice_decode as the reference calls them
+ * through _rice_compress / _rice_decompress (main.py:174-186; call sites
+ * main.py:884-885 with fallback_bits 16 for the large values and 32 for the
+ * positions, main.py:527-529 to decode, max_quotient 31).  The byte format
+ * of fast-rice 0.1.0 is not available here (third-party package, absent
+ * from the reference), so this one is this library's own: archives are
+ * self-consistent, not byte-identical with the reference's Rice blobs.
+ *
+ * Blob of n >= 1 values (uint32 v, parameters FB = fallback_bits in 1..32,
+ * MQ = max_quotient in 1..64): byte 0 = the Rice parameter k in
+ * 0..min(FB, 31), the one minimising the blob's bit count (smallest on
+ * ties); then a bit stream, least significant bit of each byte first,
+ * zero-padded to a whole byte.  Per value, q = v >> k: if q < MQ, q one
+ * bits, a zero bit and the k low bits of v (low bit first); else MQ one bits
+ * and v in FB bits (low bit first).  An empty array is the single byte 0,
+ * as _rice_compress writes it (main.py:176-177).
+ * Decoding is strict: k > min(FB, 31), a stream that ends early, or any
+ * byte or non-zero padding bit after the last value is SC_HOST_ERR_RICE. */
+
+/* Largest blob of n values (bytes). */
+int64_t sc_rice_bound(int64_t n, int32_t fallback_bits, int32_t max_quotient);
+
+/* Encode n_items arrays: item i = count[i] values at vals + off[i], every
+ * value < 2**fallback_bits (else SC_HOST_ERR_RICE_RANGE); blob i is written
+ * at out + out_off[i] (room for sc_rice_bound(count[i], ...) bytes) and its
+ * length to out_len[i]. */
+int sc_rice_encode(const uint32_t *vals, const int64_t *off, const int64_t *count, int64_t n_items,
+                   int32_t fallback_bits, int32_t max_quotient, uint8_t *out, const int64_t *out_off,
+                   int64_t *out_len, int32_t n_threads, int64_t *bad);
+
+/* Decode n_items blobs: blob i = blob_len[i] bytes at blobs[i], holding
+ * count[i] values, written to out + out_off[i]; a count of 0 reads nothing
+ * (_rice_decompress returns an empty array without reading, main.py:184-185). */
+int sc_rice_decode(const uint8_t *const *blobs, const int64_t *blob_len, const int64_t *count, int64_t n_items,
+                   int32_t fallback_bits, int32_t max_quotient, uint32_t *out, const int64_t *out_off,
+                   int32_t n_threads, int64_t *bad);
 
 #ifdef __cplusplus
 }

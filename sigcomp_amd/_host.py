@@ -23,9 +23,12 @@ ERR_OVERSIZE = 13
 ERR_COUNTS = 14
 ERR_POSITION = 15
 ERR_EMPTY_READ = 16
+ERR_RICE = 24
+ERR_RICE_RANGE = 25
 
 EXPORTED = ("sc_host_last_error", "sc_host_split_count", "sc_host_split_fill", "sc_host_reassemble",
-            "sc_host_frame", "sc_host_parse", "sc_host_parse_v")
+            "sc_host_frame", "sc_host_parse", "sc_host_parse_v", "sc_rice_bound", "sc_rice_encode",
+            "sc_rice_decode")
 
 # the exception type the reference raises for each failure
 _MESSAGES = {
@@ -37,6 +40,8 @@ _MESSAGES = {
     ERR_COUNTS: (ValueError, "small and large value counts disagree with the read length"),
     ERR_POSITION: (IndexError, "large-value position outside the read"),
     ERR_EMPTY_READ: (IndexError, "a read has no samples"),
+    ERR_RICE: (ValueError, "Invalid or truncated Rice-coded blob"),
+    ERR_RICE_RANGE: (ValueError, "value does not fit the Rice fallback width"),
 }
 
 
@@ -63,8 +68,12 @@ def lib():
         L.sc_host_frame.argtypes = [_P, _P, _P, _I64, _P, _P, _I32, _P]
         L.sc_host_parse.argtypes = [_P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I32, _P]
         L.sc_host_parse_v.argtypes = [_P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P, _I32, _P]
+        L.sc_rice_bound.argtypes = [_I64, _I32, _I32]
+        L.sc_rice_encode.argtypes = [_P, _P, _P, _I64, _I32, _I32, _P, _P, _P, _I32, _P]
+        L.sc_rice_decode.argtypes = [_P, _P, _P, _I64, _I32, _I32, _P, _P, _I32, _P]
         for name in EXPORTED[1:]:
             getattr(L, name).restype = ctypes.c_int
+        L.sc_rice_bound.restype = ctypes.c_int64
         _LIB = L
     return _LIB
 

@@ -70,6 +70,8 @@ const char *err_text(int code) {
         case SC_HOST_ERR_BAD_COUNTS: return "Invalid sample or token count in SIG2 read record";
         case SC_HOST_ERR_TRAILING_RECORDS: return "SIG2 read count disagrees with trailing file data";
         case SC_HOST_ERR_INDEX: return "Index count/size does not match the archive; rebuild the index";
+        case SC_HOST_ERR_RICE: return "Invalid or truncated Rice-coded blob";
+        case SC_HOST_ERR_RICE_RANGE: return "value does not fit the Rice fallback width";
         default: return "error";
     }
 }
@@ -539,6 +541,226 @@ int sc_sig2_read_index(const uint8_t *data, int64_t size, int64_t n_expected, in
         offsets[r] = off;
     }
     return SC_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- Rice coder
+namespace {
+
+// Bits, least significant first, into a byte buffer.
+struct BitWriter {
+    uint8_t *p;
+    uint64_t acc = 0;
+    int n = 0;
+    explicit BitWriter(uint8_t *out) : p(out) {}
+    void put(uint64_t v, int len) {   // len <= 32, n < 8 on entry
+        acc |= (v & ((1ull << len) - 1)) << n;
+        n += len;
+        while (n >= 8) {
+            *p++ = (uint8_t)acc;
+            acc >>= 8;
+            n -= 8;
+        }
+    }
+    void ones(int len) {
+        while (len > 32) {
+            put(0xFFFFFFFFull, 32);
+            len -= 32;
+        }
+        put((1ull << len) - 1, len);
+    }
+    uint8_t *flush() {   // zero padding to the byte
+        if (n > 0) *p++ = (uint8_t)acc;
+        acc = 0;
+        n = 0;
+        return p;
+    }
+};
+
+inline uint64_t shr(uint64_t x, int s) { return s >= 64 ? 0 : x >> s; }
+
+struct BitReader {
+    const uint8_t *p, *end;
+    uint64_t acc = 0;
+    int n = 0;   // valid bits in acc
+    BitReader(const uint8_t *b, const uint8_t *e) : p(b), end(e) {}
+    void refill() {
+        while (n <= 56 && p < end) {
+            acc |= (uint64_t)*p++ << n;
+            n += 8;
+        }
+    }
+    // false when the stream ends before len bits (len <= 32)
+    bool get(int len, uint32_t &v) {
+        if (n < len) refill();
+        if (n < len) return false;
+        v = len ? (uint32_t)(acc & ((1ull << len) - 1)) : 0u;
+        acc = shr(acc, len);
+        n -= len;
+        return true;
+    }
+    // unary: count of one bits before a zero bit, at most `cap` ones (no
+    // zero bit is consumed when the count reaches cap); false when the
+    // stream ends first
+    bool unary(int cap, int &q) {
+        q = 0;
+        for (;;) {
+            if (n == 0) refill();
+            if (n == 0) return false;
+            const uint64_t inv = ~acc & (n == 64 ? ~0ull : ((1ull << n) - 1));
+            const int run = inv ? __builtin_ctzll(inv) : n;   // ones available in acc
+            if (q + run >= cap) {
+                const int take = cap - q;
+                acc = shr(acc, take);
+                n -= take;
+                q = cap;
+                return true;
+            }
+            if (run < n) {   // a zero bit ends the run
+                q += run;
+                acc = shr(acc, run + 1);
+                n -= run + 1;
+                return true;
+            }
+            q += run;
+            acc = 0;
+            n = 0;
+        }
+    }
+    // the rest is zero padding of the last byte, and nothing after it
+    bool at_end() const { return p == end && n < 8 && acc == 0; }
+};
+
+int rice_kmax(int32_t fb) { return fb < 31 ? fb : 31; }
+
+// bit count of the stream of vals[0..n) with parameter k
+uint64_t rice_bits(const uint32_t *v, int64_t n, int k, int32_t fb, int32_t mq) {
+    uint64_t bits = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t q = v[i] >> k;
+        bits += q < (uint32_t)mq ? q + 1 + (uint64_t)k : (uint64_t)mq + fb;
+    }
+    return bits;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t sc_rice_bound(int64_t n, int32_t fallback_bits, int32_t max_quotient) {
+    if (n <= 0) return 1;
+    return 1 + (n * ((int64_t)max_quotient + fallback_bits) + 7) / 8;
+}
+
+int sc_rice_encode(const uint32_t *vals, const int64_t *off, const int64_t *count, int64_t n_items,
+                   int32_t fallback_bits, int32_t max_quotient, uint8_t *out, const int64_t *out_off,
+                   int64_t *out_len, int32_t n_threads, int64_t *bad) {
+    if (n_items < 0 || fallback_bits < 1 || fallback_bits > 32 || max_quotient < 1 || max_quotient > 64 ||
+        (n_items && (!off || !count || !out || !out_off || !out_len))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    const int kmax = rice_kmax(fallback_bits);
+    const uint64_t lim = fallback_bits == 32 ? 0x100000000ull : (1ull << fallback_bits);
+    parallel_for(n_items, n_threads, [&](int64_t i) {
+        const int64_t n = count[i];
+        uint8_t *o = out + out_off[i];
+        if (n <= 0) {
+            o[0] = 0;
+            out_len[i] = 1;
+            if (n < 0) fb.report(i, SC_ERR_ARG);
+            return;
+        }
+        const uint32_t *v = vals + off[i];
+        for (int64_t j = 0; j < n; ++j)
+            if ((uint64_t)v[j] >= lim) {
+                fb.report(i, SC_HOST_ERR_RICE_RANGE);
+                out_len[i] = 0;
+                return;
+            }
+        int best_k = 0;
+        uint64_t best = rice_bits(v, n, 0, fallback_bits, max_quotient);
+        for (int k = 1; k <= kmax; ++k) {
+            const uint64_t b = rice_bits(v, n, k, fallback_bits, max_quotient);
+            if (b < best) {
+                best = b;
+                best_k = k;
+            }
+        }
+        o[0] = (uint8_t)best_k;
+        BitWriter w(o + 1);
+        const uint32_t mq = (uint32_t)max_quotient;
+        for (int64_t j = 0; j < n; ++j) {
+            const uint32_t q = v[j] >> best_k;
+            if (q < mq) {
+                w.ones((int)q);
+                w.put(0, 1);
+                w.put(v[j], best_k);
+            } else {
+                w.ones(max_quotient);
+                w.put(v[j], fallback_bits);
+            }
+        }
+        out_len[i] = w.flush() - o;
+    });
+    return finish(fb, bad);
+}
+
+int sc_rice_decode(const uint8_t *const *blobs, const int64_t *blob_len, const int64_t *count, int64_t n_items,
+                   int32_t fallback_bits, int32_t max_quotient, uint32_t *out, const int64_t *out_off,
+                   int32_t n_threads, int64_t *bad) {
+    if (n_items < 0 || fallback_bits < 1 || fallback_bits > 32 || max_quotient < 1 || max_quotient > 64 ||
+        (n_items && (!blobs || !blob_len || !count || !out || !out_off))) {
+        g_err = "bad argument";
+        return SC_ERR_ARG;
+    }
+    FirstBad fb;
+    const int kmax = rice_kmax(fallback_bits);
+    parallel_for(n_items, n_threads, [&](int64_t i) {
+        const int64_t n = count[i];
+        if (n <= 0) {
+            if (n < 0) fb.report(i, SC_ERR_ARG);
+            return;
+        }
+        const uint8_t *b = blobs[i];
+        const int64_t len = blob_len[i];
+        if (len < 2 || !b || b[0] > kmax) {
+            fb.report(i, SC_HOST_ERR_RICE);
+            return;
+        }
+        const int k = b[0];
+        BitReader r(b + 1, b + len);
+        uint32_t *o = out + out_off[i];
+        for (int64_t j = 0; j < n; ++j) {
+            int q;
+            uint32_t low;
+            if (!r.unary(max_quotient, q)) {
+                fb.report(i, SC_HOST_ERR_RICE);
+                return;
+            }
+            if (q < max_quotient) {
+                if (!r.get(k, low)) {
+                    fb.report(i, SC_HOST_ERR_RICE);
+                    return;
+                }
+                if (((uint64_t)q << k) > 0xFFFFFFFFull) {   // no value of 32 bits has this quotient
+                    fb.report(i, SC_HOST_ERR_RICE);
+                    return;
+                }
+                o[j] = ((uint32_t)q << k) | low;
+            } else {
+                if (!r.get(fallback_bits, low)) {
+                    fb.report(i, SC_HOST_ERR_RICE);
+                    return;
+                }
+                o[j] = low;
+            }
+        }
+        if (!r.at_end()) fb.report(i, SC_HOST_ERR_RICE);
+    });
+    return finish(fb, bad);
 }
 
 }  // extern "C"

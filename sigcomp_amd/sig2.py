@@ -4,9 +4,9 @@ include/sigcomp_host.h).
 An archive is ``b'SIG2'``, a uint32 length and the header blob, then one
 record per read (``main.py:226-246,549-607``).  The header blob (the
 zstd-compressed pickle of the global metadata), the BLOW5 per-read metadata
-(a pickle) and the two Rice-coded blobs are opaque bytes here: they are
-produced and consumed by the caller (the reference uses ``numcodecs`` and
-``fast-rice`` for them).  The SIDX index is ``b'SIDX'``, a uint32 count and
+(a pickle) and the two Rice-coded blobs are opaque bytes here: the caller
+produces them (the Rice blobs with ``sigcomp_amd.rice.encode_split``; the
+reference uses ``numcodecs`` and ``fast-rice``).  The SIDX index is ``b'SIDX'``, a uint32 count and
 per read the 16-byte read id and the uint64 record offset
 (``main.py:1451-1502``).
 """

@@ -13,9 +13,9 @@ reassembly) do with numpy, here through libsigcomp_host.so
   and shifted right by ``lsb`` (``_lossy_encode(_reduce_lsb(...))``,
   ``main.py:862-864``), and shifted back after reassembly (``main.py:1164``).
 
-The large values and positions are Rice-coded by the third-party
-``fast-rice==0.1.0`` package in the reference (``main.py:174-186``), which is
-not part of this codec; they are returned uncoded.
+The large values and positions are returned uncoded; ``sigcomp_amd.rice``
+Rice-codes them for the archive (the reference uses the third-party
+``fast-rice==0.1.0`` package there, ``main.py:174-186``).
 """
 
 from __future__ import annotations

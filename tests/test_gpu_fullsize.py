@@ -139,10 +139,11 @@ def test_sig2_record_path_on_the_gpu(gpu, oracle_mod, int_models, name):
     """Golden reads -> split -> GPU compress (batch_inference_reads) -> SIG2
     records -> archive -> scan -> GPU decompress -> reassembly: the records'
     s-blobs are the reference's payloads and the samples come back (through
-    the lossy transform for lsb > 0).  The Rice blobs hold the raw large
-    values and gaps (the Rice format is third-party)."""
+    the lossy transform for lsb > 0).  The large values and gaps are
+    Rice-coded by sigcomp_amd.rice (this library's own blob format:
+    fast-rice 0.1.0's is third-party)."""
     import signal_ref
-    from sigcomp_amd import sig2, signal
+    from sigcomp_amd import rice, sig2, signal
     from sigcomp_amd.quant_mlp_export import QuantMLPCompression
     z = np.load(GOLDEN / "e2e_reads.npz")
     lsb = int(z[f"{name}_lsb"])
@@ -151,8 +152,7 @@ def test_sig2_record_path_on_the_gpu(gpu, oracle_mod, int_models, name):
     sp = signal.split_reads(reads, lsb)
     small = signal.reads_tokens(sp)
     s_bytes = codec.batch_inference_reads(list_of_reads=small, batch_size=20480)
-    la = [sp["large_adj"][o:o + n].tobytes() for o, n in zip(sp["large_off"], sp["n_large"])]
-    lg = [sp["large_gap"][o:o + n].tobytes() for o, n in zip(sp["large_off"], sp["n_large"])]
+    la, lg = rice.encode_split(sp)
     pod = np.zeros(len(reads), sig2.POD5_DTYPE)
     pod["read_id"] = (np.arange(len(reads))[:, None] * 7 + np.arange(16)[None, :]) % 256
     recs, _ = sig2.write_records(sig2.POD5, sp["sig0"], sp["len"], sp["n_small"], s_bytes, la, lg, pod5=pod)
@@ -164,11 +164,14 @@ def test_sig2_record_path_on_the_gpu(gpu, oracle_mod, int_models, name):
         assert blobs[i] == z[f"{name}_read{i}_sbytes"].tobytes(), i
     back = codec.batch_inference_reads(list_of_compressed_reads=blobs,
                                        list_of_lengths=[int(x) for x in sc["n_small"]], batch_size=20480)
+    # c_large = N - 1 - c_small (main.py:562)
+    n_large = sc["n_samples"].astype(np.int64) - 1 - sc["n_small"].astype(np.int64)
+    assert np.array_equal(n_large, sp["n_large"])
+    large_adj, large_gap, large_off = rice.decode_split([sig2.blob(sc, i, 1) for i in range(len(reads))],
+                                                        [sig2.blob(sc, i, 2) for i in range(len(reads))], n_large)
     split = {"sig0": sc["sig0"], "len": sc["n_samples"].astype(np.int64), "small_off": sp["small_off"],
-             "n_small": sc["n_small"].astype(np.int64),
-             "large_adj": np.frombuffer(b"".join(sig2.blob(sc, i, 1) for i in range(len(reads))), np.uint16),
-             "large_gap": np.frombuffer(b"".join(sig2.blob(sc, i, 2) for i in range(len(reads))), np.uint32),
-             "large_off": sp["large_off"], "n_large": sp["n_large"]}
+             "n_small": sc["n_small"].astype(np.int64), "large_adj": large_adj, "large_gap": large_gap,
+             "large_off": large_off, "n_large": n_large}
     out = signal.reassemble_reads(split, small=np.concatenate(back), lsb=lsb)
     for r, o in zip(reads, out):
         want = signal_ref.lossy_decode(signal_ref.prepare_signal(r, lsb), lsb) if lsb else r

@@ -24,7 +24,8 @@ def test_host_library_exports_every_declared_symbol():
     import re
     _host = _lib_or_skip()
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    names = sorted(set(re.findall(r"\b(sc_host_[a-z0-9_]+)\s*\(", text)))
+    names = sorted(set(re.findall(r"\b(sc_(?:host|rice)_[a-z0-9_]+)\s*\(", text)))
+    assert "sc_rice_encode" in names and "sc_rice_decode" in names
     lib = ctypes.CDLL(str(_host.LIB_PATH))
     assert [n for n in names if not hasattr(lib, n)] == []
     assert sorted(_host.EXPORTED) == names

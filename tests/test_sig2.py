@@ -139,11 +139,11 @@ def test_archive_round_trip_through_the_read_pipeline(oracle_mod, oracle_models)
     """synthetic reads -> split -> framed range-coded tokens (the C oracle
     codec through the batched framing path) -> records -> archive bytes ->
     header + scan + index -> parse -> decode -> reassembly == the reads.
-    The Rice blobs are replaced by the raw little-endian large values and
-    gaps (the Rice format is third-party)."""
+    The large values and gaps are Rice-coded by sigcomp_amd.rice (this
+    library's own blob format: fast-rice 0.1.0's is third-party)."""
     sig2 = _sig2()
     from test_host import _OracleCodec
-    from sigcomp_amd import signal, synth
+    from sigcomp_amd import rice, signal, synth
     from sigcomp_amd.framing import ReadFramingMixin
 
     class Codec(_OracleCodec, ReadFramingMixin):
@@ -154,8 +154,7 @@ def test_archive_round_trip_through_the_read_pipeline(oracle_mod, oracle_models)
     sp = signal.split_reads(reads)
     small = signal.reads_tokens(sp)
     s_bytes = codec.batch_inference_reads(list_of_reads=small)
-    la = [sp["large_adj"][o:o + n].tobytes() for o, n in zip(sp["large_off"], sp["n_large"])]
-    lg = [sp["large_gap"][o:o + n].tobytes() for o, n in zip(sp["large_off"], sp["n_large"])]
+    la, lg = rice.encode_split(sp)
     pod = np.zeros(len(reads), sig2.POD5_DTYPE)
     pod["read_id"] = np.arange(len(reads))[:, None] + np.arange(16)[None, :]
     recs, bounds = sig2.write_records(sig2.POD5, sp["sig0"], sp["len"], sp["n_small"], s_bytes, la, lg, pod5=pod)
@@ -171,11 +170,14 @@ def test_archive_round_trip_through_the_read_pipeline(oracle_mod, oracle_models)
     assert one["n_samples"][0] == len(reads[3])
     back = codec.batch_inference_reads(list_of_compressed_reads=[sig2.blob(sc, i, 0) for i in range(len(reads))],
                                        list_of_lengths=[int(x) for x in sc["n_small"]])
+    # c_large = N - 1 - c_small (main.py:562)
+    n_large = sc["n_samples"].astype(np.int64) - 1 - sc["n_small"].astype(np.int64)
+    assert np.array_equal(n_large, sp["n_large"])
+    large_adj, large_gap, large_off = rice.decode_split([sig2.blob(sc, i, 1) for i in range(len(reads))],
+                                                        [sig2.blob(sc, i, 2) for i in range(len(reads))], n_large)
     split = {"sig0": sc["sig0"], "len": sc["n_samples"].astype(np.int64), "small_off": sp["small_off"],
-             "n_small": sc["n_small"].astype(np.int64),
-             "large_adj": np.frombuffer(b"".join(sig2.blob(sc, i, 1) for i in range(len(reads))), np.uint16),
-             "large_gap": np.frombuffer(b"".join(sig2.blob(sc, i, 2) for i in range(len(reads))), np.uint32),
-             "large_off": sp["large_off"], "n_large": sp["n_large"]}
+             "n_small": sc["n_small"].astype(np.int64), "large_adj": large_adj, "large_gap": large_gap,
+             "large_off": large_off, "n_large": n_large}
     out = signal.reassemble_reads(split, small=np.concatenate(back))
     assert all(np.array_equal(a, b) for a, b in zip(reads, out))
 
