@@ -464,6 +464,260 @@ __device__ __forceinline__ void mlp_rows_split(const ModelDev &M, const uint8_t 
                                pk, wave, lane);
 }
 
+// ---- decoder epilogue pieces ---------------------------------------------
+//
+// The LDS and global arrays of a k_decompress workgroup that its epilogue
+// (frequency table, decoder step, state update) touches.  s_wbuf holds, per
+// row, the 64 stream words from s_wbase[r] on (refilled every 64 steps, when
+// the token ring is flushed: a row consumes at most one word per step), so
+// that the word a renormalisation shifts in is an LDS read.
+template <int R>
+struct DecCtx {
+    const uint8_t *s_act;
+    const double *s_lut;
+    uint64_t *s_lower, *s_range, *s_point;
+    int64_t *s_woff, *s_toff;
+    int32_t *s_rpos, *s_wcnt, *s_len, *s_stat, *s_cur, *s_start, *s_wbase;
+    uint32_t *s_wbuf;
+    uint8_t *s_ring;
+    uint16_t *s_apos;
+    const uint32_t *words;
+    const int64_t *word_off, *tok_off;
+    const int32_t *word_cnt, *lengths;
+    uint8_t *tokens;
+    int32_t *status;
+    int64_t n_chunks, c0;
+    bool writer;
+};
+constexpr int WBUF = 64;   // words per row in DecCtx::s_wbuf
+
+// Row r's first chunk ended with step t (16 lanes of the row, lane u): its
+// last tokens go out from the ring, its status is written, and the row's
+// second chunk (2 * n_chunks - 1 - c) starts at step t + 2 from a
+// start-of-sequence context (step t + 1 is idle for the row, so that the
+// next step's layer 0, computed beside this epilogue, is never used for
+// it).  PIPE: the ring of table addresses is reset; WB: the word buffer
+// is refilled.
+template <int R, bool PIPE, bool WB>
+__device__ __forceinline__ void dec_switch(const DecCtx<R> &c, int r, int u, int32_t t) {
+    auto apos_at = [](int rr, int32_t pos) { return (pos & (WIN - 1)) * R + rr; };
+    slot_sync();
+    const int64_t ch = c.c0 + r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - c.s_start[r];
+        if (c.writer && pg <= t && rs >= 0) c.tokens[c.s_toff[r] + rs] = c.s_ring[r * WIN + (pg & (WIN - 1))];
+        if constexpr (PIPE) c.s_apos[apos_at(r, 4 * u + k)] = (uint16_t)emb_off(SOS, 0);
+    }
+    const int64_t c2 = 2 * c.n_chunks - 1 - ch;
+    const int32_t cnt = c.word_cnt[c2];
+    const int64_t woff = c.word_off[c2];
+    int take;
+    const uint64_t point = dec_init_point(c.words + woff, cnt, take);
+    if (u == 0) {
+        if (c.writer) c.status[ch] = c.s_stat[r];
+        c.s_point[r] = point;
+        c.s_lower[r] = 0ull;
+        c.s_range[r] = ~0ull;
+        c.s_rpos[r] = take;
+        c.s_stat[r] = 0;
+        c.s_wcnt[r] = cnt;
+        c.s_woff[r] = woff;
+        c.s_toff[r] = c.tok_off[c2];
+        c.s_len[r] = c.lengths[c2];
+        c.s_cur[r] = 3;
+        c.s_start[r] = t + 2;
+        if constexpr (WB) c.s_wbase[r] = take;
+    }
+    if constexpr (WB) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * u + k;
+            c.s_wbuf[r * WBUF + i] = take + i < cnt ? c.words[woff + take + i] : 0u;
+        }
+    }
+}
+
+// The decoder epilogue of one step for one group of four rows per wave
+// (row 4 * (wave + 4 q) + lane / 16), cut into straight-line pieces for
+// gemm_layer0_ov: piece<I>(q) runs in k-step region I of body q, after<I>
+// between regions (the rare paths).  Each piece's LDS reads are used in a
+// later piece (a region starts with a wait for all of them).  The
+// arithmetic is row_freq's and the k_decompress epilogue's for one row
+// (_frequencies and _decode_partition, cpu_entropy_coding.py:90-110,230-266).
+template <int R, bool PIPE>
+struct DecEpiSide {
+    const DecCtx<R> &c;
+    uint32_t *slot;          // the row's slot (SLOT_DWORDS)
+    int32_t t;
+    int wave, q4, u;
+    uint32_t lanebits;
+    int r;
+    int32_t rs, len, stat, cur, start, rpos, wcnt, wbase;
+    uint64_t lower, range, point;
+    uint32_t wnext, mcum, mkfix, mffix, mown, fs;
+    v4i raw;
+    bool active, last1, ok;
+    int lm, m;
+    double wv[8];
+    double T, r24;
+    RowFreq fr;
+    uint32_t hmin, S, K, qv;
+
+    __device__ DecEpiSide(const DecCtx<R> &ctx, uint32_t *wave_slots, int32_t t_, int wave_, int lane)
+        : c(ctx), slot(wave_slots + (lane >> 4) * SLOT_DWORDS), t(t_), wave(wave_), q4(lane >> 4), u(lane & 15),
+          lanebits((uint32_t)(15 - (lane & 15)) << 4) {}
+
+    __device__ __forceinline__ int logit(int k) const {
+        return (int)(int8_t)((uint32_t)raw[k >> 2] >> (8 * (k & 3)));
+    }
+    __device__ __forceinline__ void lut8(int k0) {
+        const double *p = c.s_lut + (VOCAB - 1 - m);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) wv[k] = p[logit(k0 + k)];
+    }
+    __device__ __forceinline__ double sum8() const {
+        return ((wv[0] + wv[1]) + (wv[2] + wv[3])) + ((wv[4] + wv[5]) + (wv[6] + wv[7]));
+    }
+    __device__ __forceinline__ void freq8(int k0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const double qe = __builtin_fmax(__builtin_fma(wv[k], r24, 0x1p-20), 1.5);
+            fr.f[k0 + k] = (uint32_t)qe;
+            hmin = min(hmin, (uint32_t)(__builtin_bit_cast(uint64_t, __builtin_amdgcn_fract(qe)) >> 32));
+        }
+    }
+
+    template <int I>
+    __device__ __forceinline__ void piece(int q) {
+        if constexpr (I == 0) {
+            r = ((wave + q * WAVES) << 2) + q4;
+            start = c.s_start[r];
+            len = c.s_len[r];
+            stat = c.s_stat[r];
+            cur = c.s_cur[r];
+            lower = c.s_lower[r];
+            range = c.s_range[r];
+            point = c.s_point[r];
+            rpos = c.s_rpos[r];
+            wcnt = c.s_wcnt[r];
+            wbase = c.s_wbase[r];
+            raw = *(const v4i *)(c.s_act + act_at<PIPE>(r, u));
+        } else if constexpr (I == 1) {
+            rs = t - start;
+            active = rs >= 0 && rs < len && stat == 0;
+            last1 = cur == 2 && rs == len - 1;   // the row's first chunk ends with this step
+            wnext = c.s_wbuf[r * WBUF + ((rpos - wbase) & (WBUF - 1))];
+            lm = logit(0);
+#pragma unroll
+            for (int k = 1; k < 16; ++k) lm = max(lm, logit(k));
+        } else if constexpr (I == 2) {
+            m = row16_max(lm);
+            lut8(0);
+        } else if constexpr (I == 3) {
+            T = sum8();
+            lut8(8);
+        } else if constexpr (I == 4) {
+            T = row16_sum_f64(T + sum8());
+        } else if constexpr (I == 5) {
+            r24 = recip_nr(T) * 16777216.0;
+            lut8(0);
+        } else if constexpr (I == 6) {
+            hmin = 0xFFFFFFFFu;
+            freq8(0);
+            lut8(8);
+        } else if constexpr (I == 7) {
+            freq8(8);
+        } else if constexpr (I == 8) {
+            uint32_t sl = 0, km = 0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                sl += fr.f[k];
+                km = max(km, (fr.f[k] << 4) | (uint32_t)(15 - k));
+            }
+            fr.tot = sl;
+            S = sl;
+            K = (((km << 4) - 256u) & 0xFFFFFF00u) | lanebits | (km & 15u);
+        } else if constexpr (I == 9) {
+            S = row16_sum(S);
+            K = row16_max_u32(K);
+        } else if constexpr (I == 10) {
+            const uint32_t adj = S - TOTAL;
+            const bool star = (K & 0xF0u) == lanebits;
+            fr.ffix = (K >> 8) + 1u - adj;
+            fr.kfix = star ? 15u - (K & 15u) : 16u;
+            if (star) fr.tot -= adj;
+            fr.ex = row16_excl_scan(fr.tot);
+        } else if constexpr (I == 11) {
+            const uint64_t scale = range >> 24;
+            qv = 0;
+            ok = scale != 0 && dec_quantile(point - lower, scale, qv);
+        } else if constexpr (I == 12) {
+            if (ok && qv - fr.ex < fr.tot) slot_put(slot, fr, u);
+        } else if constexpr (I == 13) {
+            // slot_get's reads (used in the next piece)
+            slot_sync();
+            typedef unsigned v4u __attribute__((ext_vector_type(4)));
+            const v4u meta = *(const v4u *)(slot + 16);
+            mcum = meta[0];
+            mkfix = meta[1];
+            mffix = meta[2];
+            mown = meta[3];
+            fs = slot[u];
+        } else if constexpr (I == 14) {
+            const uint32_t fq = (uint32_t)u == mkfix ? mffix : fs;
+            const uint32_t cum = mcum + row16_excl_scan(fq);
+            if (active && ok && qv - cum < fq) {
+                const uint64_t scale = range >> 24;
+                uint64_t lo = lower + mul_scale(scale, cum), ra = mul_scale(scale, fq), pt = point;
+                int32_t rp = rpos;
+                if (ra < (1ull << 32)) {
+                    lo <<= 32;
+                    ra <<= 32;
+                    pt = (pt << 32) | (rpos < wcnt ? wnext : 0u);
+                    rp += 1;
+                }
+                c.s_lower[r] = lo;
+                c.s_range[r] = ra;
+                c.s_point[r] = pt;
+                c.s_rpos[r] = rp;
+                const int sym = (int)mown * 16 + u;
+                c.s_ring[r * WIN + (t & (WIN - 1))] = (uint8_t)sym;
+                if constexpr (PIPE) c.s_apos[(t & (WIN - 1)) * R + r] = (uint16_t)emb_off(sym, 0);
+            }
+            if (active && !ok && u == 0) c.s_stat[r] = SC_STATUS_INVALID_STREAM;
+        }
+    }
+
+    template <int I>
+    __device__ __forceinline__ void after(int) {
+        if constexpr (I == 7) {
+            // high word of 2**-19: the float64 estimate of a frequency is
+            // within 2**-19 of an integer -> exact integer division
+            if (hmin < 0x3EC00000u) {
+                const uint64_t Ti = (uint64_t)T;
+                const double rT = r24 * 0x1p-24;
+                const double *p = c.s_lut + (VOCAB - 1 - m);
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const uint64_t qd = div_floor_est(((uint64_t)p[logit(k)]) << 24, Ti, rT);
+                    fr.f[k] = qd < 1 ? 1u : (uint32_t)qd;
+                }
+            }
+        } else if constexpr (I == 15) {
+            if (last1) dec_switch<R, PIPE, true>(c, r, u, t);
+        }
+    }
+};
+
+// No side work (gemm_layer0_ov with ng = 0).
+struct NoSide {
+    template <int I>
+    __device__ __forceinline__ void piece(int) {}
+    template <int I>
+    __device__ __forceinline__ void after(int) {}
+};
+
 // P = 1: workgroup b owns chunks [b*R, b*R + R) and never synchronises with
 // another.  P > 1 (RT = 1, pipelined per-tensor core): the split decode
 // above, workgroup b being slice b % P of the group of chunks
@@ -487,6 +741,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     static_assert(P == 1 || (RT == 1 && CORE == CORE_PIPE_UNI), "the split decode runs 32-row groups on the per-tensor core");
     static_assert(P == 1 || P == 4 || P == 8, "split decode: 4 or 8 workgroups per group");
     constexpr bool PIPE = CORE != CORE_PLAIN;
+    // the epilogue beside the next step's layer 0 (gemm_layer0_ov)
+    constexpr bool OV = P == 1 && PIPE && RT >= 2 && RT <= 3;
     constexpr int R = 32 * RT;
     constexpr int EPI_N = 2;   // row groups per epilogue iteration; R / 4 is a multiple of EPI_N * WAVES
     static_assert((R / 4) % (EPI_N * WAVES) == 0, "epilogue iterations must cover the rows exactly");
@@ -509,6 +765,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
     // which chunk of the row is current (bit 0: the second one; bit 1: the
     // row has a second chunk) and the step at which it started
     __shared__ int32_t s_cur[R], s_start[R];
+    __shared__ uint32_t s_wbuf[OV ? R * WBUF : 1];
+    __shared__ int32_t s_wbase[OV ? R : 1];
     __shared__ int32_t s_maxlen, s_xerr;
     __shared__ int32_t s_red[P == 8 ? 2 * 16 * 64 : 1];   // partial layer-0 sums of the split decode
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -532,7 +790,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         const bool paired = PIPE && in && c >= n_chunks - n_second;
         const int32_t len1 = in ? lengths[c] : 0;
         const int32_t len2 = paired ? lengths[2 * n_chunks - 1 - c] : 0;
-        atomicMax(&s_maxlen, max(len1, 0) + max(len2, 0));
+        // (a second chunk starts one step after the first ends)
+        atomicMax(&s_maxlen, max(len1, 0) + max(len2, 0) + (paired && len1 > 0 ? 1 : 0));
     }
     __syncthreads();
     const int32_t maxlen = s_maxlen;
@@ -608,25 +867,11 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
         }
         __syncthreads();
     }
-    L0Carry l0c;   // (split decode) layer 0 carried between steps
-    l0c.have = false;
-    for (int32_t t = t_begin; t < t_stop; ++t) {
-        auto apos = [&](int r, int p) {
-            if (t + p < WIN) return emb_off(SOS, 0);
-            if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
-            else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
-        };
-        if constexpr (P > 1) {
-            // the next step's window, of which all but the last position is known
-            auto apos_next = [&](int r, int p) {
-                if (t + 1 + p < WIN) return emb_off(SOS, 0);
-                return (int)s_apos[apos_at(r, t + 1 + p)];
-            };
-            mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, apos_next, t + 1 < t_stop, l0c, wave, lane,
-                              xch + group * XCH_GROUP, (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P,
-                              slice, t, spin_max, &s_xerr, s_red);
-        } else
-            mlp_tile<CORE, RT>(M, s_emb, s_act, s_par, apos, wave, lane);
+    const DecCtx<R> ctx{s_act, s_lut, s_lower, s_range, s_point, s_woff, s_toff, s_rpos, s_wcnt, s_len, s_stat,
+                        s_cur, s_start, s_wbase, s_wbuf, s_ring, s_apos, words, word_off, tok_off, word_cnt,
+                        lengths, tokens, status, n_chunks, c0, writer};
+    // the epilogue of step t (EPI_N row groups per iteration)
+    auto epilogue = [&](int32_t t) {
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.
         // _decode_partition (cpu_entropy_coding.py:230-266): every lane of a
         // row computes the row's quantile; the lane whose 16 symbols hold it
@@ -648,7 +893,7 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                 const int r = (gi + n * WAVES) * 4 + q4;
                 rr[n] = r;
                 const int32_t rs = t - s_start[r], len = s_len[r];
-                active[n] = rs < len && s_stat[r] == 0;
+                active[n] = rs >= 0 && rs < len && s_stat[r] == 0;
                 last1[n] = s_cur[r] == 2 && rs == len - 1;   // the row's first chunk ends with this step
                 lower[n] = s_lower[r];
                 range[n] = s_range[r];
@@ -692,40 +937,12 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                     if constexpr (PIPE) s_apos[apos_at(r, t)] = (uint16_t)emb_off(owner * 16 + u, 0);
                 }
                 if (active[n] && !ok[n] && u == 0) s_stat[r] = SC_STATUS_INVALID_STREAM;
-                if (last1[n]) {
-                    // write out the first chunk's last tokens, then start the
-                    // second chunk from the next step with a start-of-sequence
-                    // context
-                    slot_sync();
-                    const int64_t c = c0 + r;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int32_t pg = (t & ~(WIN - 1)) + 4 * u + k, rs = pg - s_start[r];
-                        if (writer && pg <= t && rs >= 0) tokens[s_toff[r] + rs] = s_ring[r * WIN + (pg & (WIN - 1))];
-                        if constexpr (PIPE) s_apos[apos_at(r, 4 * u + k)] = (uint16_t)emb_off(SOS, 0);
-                    }
-                    if (u == 0) {
-                        if (writer) status[c] = s_stat[r];
-                        const int64_t c2 = 2 * n_chunks - 1 - c;
-                        const int32_t cnt = word_cnt[c2];
-                        const int64_t woff = word_off[c2];
-                        int take;
-                        s_point[r] = dec_init_point(words + woff, cnt, take);
-                        s_lower[r] = 0ull;
-                        s_range[r] = ~0ull;
-                        s_rpos[r] = take;
-                        s_stat[r] = 0;
-                        s_wcnt[r] = cnt;
-                        s_woff[r] = woff;
-                        s_toff[r] = tok_off[c2];
-                        s_len[r] = lengths[c2];
-                        s_cur[r] = 3;
-                        s_start[r] = t + 1;
-                    }
-                }
+                if (last1[n]) dec_switch<R, PIPE, OV>(ctx, r, u, t);
             }
         }
-        __syncthreads();
+    };
+    // the end of step t (after the barrier that ends its epilogue)
+    auto flush = [&](int32_t t) {
         // every 64 steps (and at the end) the ring holds the last 64 tokens
         // of each chunk: one wavefront per chunk writes them as one 64-byte
         // run instead of a byte per step
@@ -735,6 +952,82 @@ __global__ __launch_bounds__(THREADS, 1) void k_decompress(ModelDev M, const uin
                 const int32_t rs = p - s_start[r];
                 if (p <= t && rs >= 0 && rs < s_len[r]) tokens[s_toff[r] + rs] = s_ring[r * WIN + lane];
             }
+        }
+        if constexpr (OV) {
+            // the next 64 words of every row
+            if ((t & (WIN - 1)) == WIN - 1) {
+                for (int r = wave; r < R; r += WAVES) {
+                    const int32_t base = s_rpos[r], cnt = s_wcnt[r];
+                    s_wbuf[r * WBUF + lane] = base + lane < cnt ? words[s_woff[r] + base + lane] : 0u;
+                    if (lane == 0) s_wbase[r] = base;
+                }
+            }
+        }
+    };
+    if constexpr (OV) {
+        // Step t: the MLP after layer 0 (pipe_rest), then layer 0 of step
+        // t + 1 with step t's epilogue beside it and, between its last two
+        // positions, the barrier that publishes step t's symbols and the
+        // end of step t.  The segment's first layer 0 runs alone, its last
+        // epilogue after the MLP.
+        constexpr bool UNI = CORE == CORE_PIPE_UNI;
+        constexpr int NG = R / 16;              // row groups of four rows per wave
+        constexpr int XV = RT >= 3 ? 4 : 6;     // side VALU per MFMA
+        v16i accA[PNT][RT], accB[PNT][RT];
+        uint32_t prl[Slot<UNI>::LANE];
+        int32_t tl0 = t_begin;                  // the step of the layer 0 in flight
+        auto apos0 = [&](int r, int p) {
+            if (tl0 + p < WIN) return emb_off(SOS, 0);
+            return (int)s_apos[apos_at(r, tl0 + p)];
+        };
+        for (int r = wave; r < R; r += WAVES) {
+            const int32_t base = s_rpos[r], cnt = s_wcnt[r];
+            s_wbuf[r * WBUF + lane] = base + lane < cnt ? words[s_woff[r] + base + lane] : 0u;
+            if (lane == 0) s_wbase[r] = base;
+        }
+        {
+            NoSide none;
+            pipe_layer0_ov<RT, UNI, XV>(M, s_emb, s_par, apos0, accA, accB, prl, wave, lane, 0, none, [] {});
+        }
+        uint32_t *wslots = s_slot + wave * (EPI_N * 4 * SLOT_DWORDS);
+        for (int32_t t = t_begin; t < t_stop; ++t) {
+            pipe_rest<RT, UNI>(M, s_act, s_par, accA, accB, prl, wave, lane);
+            if (t + 1 < t_stop) {
+                tl0 = t + 1;
+                DecEpiSide<R, PIPE> side(ctx, wslots, t, wave, lane);
+                pipe_layer0_ov<RT, UNI, XV>(M, s_emb, s_par, apos0, accA, accB, prl, wave, lane, NG, side, [&] {
+                    __syncthreads();
+                    flush(t);
+                });
+            } else {
+                epilogue(t);
+                __syncthreads();
+                flush(t);
+            }
+        }
+    } else {
+        L0Carry l0c;   // (split decode) layer 0 carried between steps
+        l0c.have = false;
+        for (int32_t t = t_begin; t < t_stop; ++t) {
+            auto apos = [&](int r, int p) {
+                if (t + p < WIN) return emb_off(SOS, 0);
+                if constexpr (PIPE) return (int)s_apos[apos_at(r, t + p)];
+                else return emb_off(s_ring[r * WIN + ((t + p) & (WIN - 1))], 0);
+            };
+            if constexpr (P > 1) {
+                // the next step's window, of which all but the last position is known
+                auto apos_next = [&](int r, int p) {
+                    if (t + 1 + p < WIN) return emb_off(SOS, 0);
+                    return (int)s_apos[apos_at(r, t + 1 + p)];
+                };
+                mlp_rows_split<P>(M, s_emb, s_act, s_par, apos, apos_next, t + 1 < t_stop, l0c, wave, lane,
+                                  xch + group * XCH_GROUP, (int32_t *)(xch + (int64_t)gridDim.x / P * XCH_GROUP) + group * P,
+                                  slice, t, spin_max, &s_xerr, s_red);
+            } else
+                mlp_tile<CORE, RT>(M, s_emb, s_act, s_par, apos, wave, lane);
+            epilogue(t);
+            __syncthreads();
+            flush(t);
         }
     }
     if (!writer) return;

@@ -122,8 +122,11 @@ __global__ __launch_bounds__(1024) void k_dec_lengths(const int32_t *__restrict_
         if (i >= g0 && i < g0 + G) m[2] = max(m[2], l);
         if (i >= g0 + G && i < g0 + G + left) m[3] = max(m[3], l);
     }
-    for (int64_t i = threadIdx.x; i < left; i += 1024)
-        m[1] = max(m[1], max(lengths[g0 + G - left + i], 0) + max(lengths[g0 + G + left - 1 - i], 0));
+    // a pair's second chunk starts one step after its first ends
+    for (int64_t i = threadIdx.x; i < left; i += 1024) {
+        const int32_t l1 = max(lengths[g0 + G - left + i], 0);
+        m[1] = max(m[1], l1 + max(lengths[g0 + G + left - 1 - i], 0) + (l1 > 0 ? 1 : 0));
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         m[k] = wave_max_i32(m[k]);
@@ -867,16 +870,20 @@ int64_t sc_decompress_workspace_bytes(int64_t n_chunks) {
 }
 
 // The launch plan's length statistics on the host (k_dec_lengths' rule):
-// [0] longest chunk, [1] longest pair (row g0+G-left+i followed by chunk
-// g0+G+left-1-i), [2] longest chunk of the last full-wave launch
-// (g0 .. g0+G-1), [3] longest leftover chunk; negative lengths count as 0.
+// [0] longest chunk, [1] most steps of a pair (row g0+G-left+i followed by
+// chunk g0+G+left-1-i, which starts one step after the first ends), [2]
+// longest chunk of the last full-wave launch (g0 .. g0+G-1), [3] longest
+// leftover chunk; negative lengths count as 0.
 static void host_len_stats(const int32_t *len, int64_t n, int64_t g0, int64_t G, int64_t left, int32_t out[4]) {
     auto at = [&](int64_t i) { return std::max(len[i], 0); };
     out[0] = out[1] = out[2] = out[3] = 0;
     for (int64_t i = 0; i < n; ++i) out[0] = std::max(out[0], at(i));
     for (int64_t i = g0; i < g0 + G && i < n; ++i) out[2] = std::max(out[2], at(i));
     for (int64_t i = g0 + G; i < g0 + G + left && i < n; ++i) out[3] = std::max(out[3], at(i));
-    for (int64_t i = 0; i < left; ++i) out[1] = std::max(out[1], at(g0 + G - left + i) + at(g0 + G + left - 1 - i));
+    for (int64_t i = 0; i < left; ++i) {
+        const int32_t l1 = at(g0 + G - left + i);
+        out[1] = std::max(out[1], l1 + at(g0 + G + left - 1 - i) + (l1 > 0 ? 1 : 0));
+    }
 }
 
 // The decode of sc_decompress_chunks with its buffers given: `state` holds

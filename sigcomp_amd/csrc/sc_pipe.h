@@ -510,6 +510,225 @@ __device__ __forceinline__ v16i gemm_layer0_position(const v4i *wp, int p, const
     return acc;
 }
 
+// ---- layer 0 overlapped with the decoder's epilogue ---------------------
+//
+// The window of decode step t+1 holds 63 tokens known before step t's
+// symbol; only its last position needs that symbol.  gemm_layer0_ov runs
+// layer 0 of step t+1 (mlp_rows_pipe's one-pass form over both passes'
+// n-tiles) with side work in its first positions and a hook before the
+// last one:
+//
+//   positions 0 .. 4*ng-1 in ng bodies of four positions (16 k-steps): in
+//     k-step I of body q, side.template piece<I>(q) runs in the same
+//     scheduling region as the k-step's MFMAs (instruction groups of one
+//     MFMA and XV other VALU), then side.template after<I>(q) (the side
+//     work's rare paths: wave-uniform branches between regions);
+//   positions 4*ng .. 62 plain;
+//   mid() (the caller's barrier that publishes step t's symbols);
+//   position 63, its table addresses read after mid().
+//
+// Every k-step region starts with an s_waitcnt for all LDS reads of the
+// wave (this k-step's B fragments), so a side piece's LDS reads are
+// complete in the next region without a wait of their own.  Weight
+// fragments are loaded PD = 4 k-steps ahead across the whole range; the
+// first k-step accumulates onto init().
+template <int XV, int NTP, int RT>
+__device__ __forceinline__ void kstep_schedule_side() {
+    // LDS reads (the next k-step's B fragments and the side piece's) go in
+    // the groups after the first MFMAs, their address arithmetic in the
+    // VALU groups before them, so that they complete well before the next
+    // region's wait; weight loads and the rest of the side work follow
+    static_for<NTP * RT>([&](auto mc) __attribute__((always_inline)) {
+        constexpr int m = decltype(mc)::value;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                   // MFMA
+        if constexpr (m >= 1 && m <= 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // LDS reads
+        if constexpr (m >= 2 && m < 2 + NTP) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // weight load
+        __builtin_amdgcn_sched_group_barrier(0x002, XV, 0);                                  // side work
+    });
+}
+
+template <int NTP, int RT, int XV, class AposFn, class NtFn, class AccFn, class InitFn, class Side, class Mid>
+__device__ __forceinline__ void gemm_layer0_ov(const WStream &ws, NtFn nt, const uint8_t *s_emb, AposFn apos,
+                                               AccFn acc, InitFn init, int lane, int ng, Side &side, Mid &&mid) {
+    constexpr int PD = 4;
+    static_assert(EDIM / 32 == PD && WIN == 64, "four k-steps per position, 64 positions");
+    int voff[NTP];
+#pragma unroll
+    for (int j = 0; j < NTP; ++j) voff[j] = nt(j) * KT0 * 1024 + lane * 16;
+    v4i w[2][PD][NTP];
+#pragma unroll
+    for (int s = 0; s < PD; ++s)
+#pragma unroll
+        for (int j = 0; j < NTP; ++j) w[0][s][j] = wload(ws, voff[j], s);
+    const int rl = lane & 31, kg = (lane >> 5) << 4;
+    // ea[x]: this lane's B address of the position with parity x; an[x]: the
+    // table address of the next position with parity x (read two ahead)
+    int ea[2][RT], an[2][RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        ea[0][i] = apos(i * 32 + rl, 0) + kg;
+        an[1][i] = apos(i * 32 + rl, 1);
+    }
+    v4i b[2][RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) b[0][i] = *(const v4i *)(s_emb + ea[0][i]);
+    // k-step S of position p (parity H); FIRST: from init(); PIECE >= 0: with
+    // that side piece; NEXTB = false: no B read of the next position
+    auto kstep = [&](int p, int q, auto hc, auto sc, auto firstc, auto piecec, auto nextbc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value, s = decltype(sc)::value, hn = h ^ 1;
+        constexpr bool FIRST = decltype(firstc)::value, NEXTB = decltype(nextbc)::value;
+        constexpr int PIECE = decltype(piecec)::value;
+        constexpr int bc = s & 1, bn = bc ^ 1;
+        const int kt = p * PD + s;
+        wait_counts<NTP * (PD - 1), 0>();
+        if constexpr (s == 0) {
+            const int p2 = p + 2 < WIN ? p + 2 : WIN - 1;
+#pragma unroll
+            for (int i = 0; i < RT; ++i) an[h][i] = apos(i * 32 + rl, p2);
+        }
+        if constexpr (s + 1 < PD) {
+#pragma unroll
+            for (int i = 0; i < RT; ++i) b[bn][i] = *(const v4i *)(s_emb + ea[h][i] + (s + 1) * 32);
+        } else if constexpr (NEXTB) {
+#pragma unroll
+            for (int i = 0; i < RT; ++i) b[bn][i] = *(const v4i *)(s_emb + ea[hn][i]);
+        }
+#pragma unroll
+        for (int j = 0; j < NTP; ++j) w[hn][s][j] = wload(ws, voff[j], kt + PD);
+#pragma unroll
+        for (int j = 0; j < NTP; ++j)
+#pragma unroll
+            for (int i = 0; i < RT; ++i) {
+                v16i &a = acc(j, i);
+                a = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[h][s][j], b[bc][i], FIRST && s == 0 ? init(j, i) : a,
+                                                          0, 0, 0);
+            }
+        if constexpr (PIECE >= 0) {
+            side.template piece<PIECE>(q);
+            kstep_schedule_side<XV, NTP, RT>();
+        } else {
+            kstep_schedule<NTP, RT>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PIECE >= 0) side.template after<PIECE>(q);
+    };
+    using F = std::false_type;
+    using T = std::true_type;
+    // position p (parity H): its next position's addresses first
+    auto position = [&](int p, int q, auto hc, auto firstc, auto piece0c, auto nextbc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value, hn = h ^ 1, P0 = decltype(piece0c)::value;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) ea[hn][i] = an[hn][i] + kg;
+        auto pc = [](auto sc) { return std::integral_constant<int, P0 < 0 ? -1 : P0 + decltype(sc)::value>{}; };
+        kstep(p, q, hc, std::integral_constant<int, 0>{}, firstc, pc(std::integral_constant<int, 0>{}), T{});
+        kstep(p, q, hc, std::integral_constant<int, 1>{}, F{}, pc(std::integral_constant<int, 1>{}), T{});
+        kstep(p, q, hc, std::integral_constant<int, 2>{}, F{}, pc(std::integral_constant<int, 2>{}), T{});
+        kstep(p, q, hc, std::integral_constant<int, 3>{}, F{}, pc(std::integral_constant<int, 3>{}), nextbc);
+    };
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    using NP = std::integral_constant<int, -1>;
+    // a body: four positions with side pieces 0..15
+    auto body = [&](int q, auto firstc) __attribute__((always_inline)) {
+        const int p0 = 4 * q;
+        position(p0, q, H0{}, firstc, std::integral_constant<int, 0>{}, T{});
+        position(p0 + 1, q, H1{}, F{}, std::integral_constant<int, 4>{}, T{});
+        position(p0 + 2, q, H0{}, F{}, std::integral_constant<int, 8>{}, T{});
+        position(p0 + 3, q, H1{}, F{}, std::integral_constant<int, 12>{}, T{});
+    };
+    int pbeg = 0;
+    if (ng > 0) {
+        body(0, T{});
+#pragma unroll 1
+        for (int q = 1; q < ng; ++q) body(q, F{});
+        pbeg = 4 * ng;
+    } else {
+        position(0, 0, H0{}, T{}, NP{}, T{});
+        position(1, 0, H1{}, F{}, NP{}, T{});
+        pbeg = 2;
+    }
+#pragma unroll 1
+    for (int p0 = pbeg; p0 < WIN - 2; p0 += 2) {
+        position(p0, 0, H0{}, F{}, NP{}, T{});
+        position(p0 + 1, 0, H1{}, F{}, NP{}, T{});
+    }
+    position(WIN - 2, 0, H0{}, F{}, NP{}, F{});
+    mid();
+    // position 63: its table addresses and first B fragments now
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        ea[1][i] = apos(i * 32 + rl, WIN - 1) + kg;
+        b[0][i] = *(const v4i *)(s_emb + ea[1][i]);
+    }
+    // (position()'s own first statement would overwrite ea[1] from the
+    // stale an[1]: the k-steps are issued directly)
+    kstep(WIN - 1, 0, H1{}, std::integral_constant<int, 0>{}, F{}, NP{}, T{});
+    kstep(WIN - 1, 0, H1{}, std::integral_constant<int, 1>{}, F{}, NP{}, T{});
+    kstep(WIN - 1, 0, H1{}, std::integral_constant<int, 2>{}, F{}, NP{}, T{});
+    kstep(WIN - 1, 0, H1{}, std::integral_constant<int, 3>{}, F{}, NP{}, F{});
+}
+
+// Layer 0 of mlp_rows_pipe with the epilogue of the previous decode step
+// beside it (gemm_layer0_ov): accA / accB receive both passes' layer-0
+// accumulators (bias included), pr the first hidden layer's pass-0
+// parameter block (pipe_rest stores it).
+template <int RT, bool UNI, int XV, class AposFn, class Side, class Mid>
+__device__ __forceinline__ void pipe_layer0_ov(const ModelDev &M, const uint8_t *s_emb, const uint32_t *s_par,
+                                               AposFn apos, v16i (&accA)[PNT][RT], v16i (&accB)[PNT][RT],
+                                               uint32_t (&pr)[Slot<UNI>::LANE], int wave, int lane, int ng,
+                                               Side &side, Mid &&mid) {
+    wave = __builtin_amdgcn_readfirstlane(wave);
+    const int nb0 = 2 * wave, nb1 = 8 + 2 * wave, g = lane >> 5;
+    constexpr int BLK = Slot<UNI>::BLK;
+    const uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
+    const uint32_t *p00 = s_parw + slot_p0(0) * BLK, *p10 = s_parw + slot_p1(0) * BLK;
+    par_fetch<UNI>(M.layer[1].par, nb0, lane, pr);
+    const LayerDev &L0 = M.layer[0];
+    const WStream ws = make_wstream(L0.w, L0.bytes);
+    gemm_layer0_ov<2 * PNT, RT, XV>(
+        ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, apos,
+        [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; },
+        [&](int j, int) { return j < PNT ? bias_tile<UNI>(p00, j, g) : bias_tile<UNI>(p10, j - PNT, g); }, lane, ng,
+        side, mid);
+}
+
+// mlp_rows_pipe after its layer 0 (accA / accB from pipe_layer0_ov, pr its
+// parameter block): entered when no wave reads s_act any more, leaves the
+// logits in s_act after a barrier.
+template <int RT, bool UNI>
+__device__ __forceinline__ void pipe_rest(const ModelDev &M, uint8_t *s_act, uint32_t *s_par, v16i (&accA)[PNT][RT],
+                                          v16i (&accB)[PNT][RT], const uint32_t (&pr)[Slot<UNI>::LANE], int wave,
+                                          int lane) {
+    wave = __builtin_amdgcn_readfirstlane(wave);
+    const int voff = lane * 16;
+    const int nb0 = 2 * wave;
+    constexpr int BLK = Slot<UNI>::BLK;
+    uint32_t *s_parw = s_par + wave * PIPE_SLOTS * BLK;
+    constexpr int PPD = ppd<RT>();
+    v4i w[2][PPD][PNT];
+    uint32_t pk[PNT][RT][4];
+    {
+        const LayerDev &L0 = M.layer[0];
+        par_put<UNI>(s_parw + slot_p0(1) * BLK, pr, lane);
+        if constexpr (UNI) rq_pass_uni<true, RT>(accA, rq_uni(L0), pk);
+        else requant_pack_t<PNT, RT, true, true, false>(accA, s_parw + slot_p0(0) * BLK, lane, pk);
+        pstore_perm<RT>(pk, nb0, s_act, lane);
+        const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
+#pragma unroll
+        for (int s = 0; s < PPD; ++s)
+#pragma unroll
+            for (int j = 0; j < PNT; ++j) w[0][s][j] = wload_s(rs1, voff, ((nb0 + j) * KTH + s) * 1024);
+        __syncthreads();
+    }
+    const int last = M.n_layers - 1;
+#pragma unroll 1
+    for (int l = 1; l < last; ++l)
+        pipe_hidden<RT, false, UNI>(M.layer[l - 1], M.layer[l], M.layer[l + 1], s_act, s_parw, l, accA, accB, w, pk,
+                                    wave, lane);
+    pipe_hidden<RT, true, UNI>(M.layer[last - 1], M.layer[last], M.layer[last], s_act, s_parw, last, accA, accB, w,
+                               pk, wave, lane);
+}
+
 // One MLP evaluation of R = 32*RT rows (RT <= 4), same contract as mlp_rows
 // but in the padded row layout: entered after a barrier that ends every read
 // of s_act (R * PACT_ROW bytes), leaves the int8 logits in bytes 0..255 of

@@ -633,6 +633,36 @@ def test_decompress_paired_rows_status_and_edges(codecs, capfd, monkeypatch, seg
             assert np.array_equal(back[s], tokens[s]), i
 
 
+@pytest.mark.parametrize("seg, host", [(None, True), (64, True), (0, True), (64, False)])
+def test_decompress_longest_row_is_a_pair_ending_on_a_segment_edge(codecs, capfd, monkeypatch, seg, host):
+    """A paired row's second chunk starts one step after its first ends, so
+    a pair of 24 + 1000 tokens takes 1025 steps: more than the longest
+    single chunk (1000) and one past a 64- and 256-step segment edge.  The
+    launch plan counts that step (its last token decodes) in 96-chunk
+    workgroups, whose epilogue runs beside the next step's layer 0; with
+    the plan's length statistics from the host copy of the lengths or from
+    the device."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    G, L = 3 * 32 * n_cu, 50
+    rng = np.random.default_rng(5 + (seg or 0))
+    lengths = np.concatenate([rng.integers(900, 1001, G - L), rng.integers(100, 401, L),
+                              rng.integers(1, 101, L)]).astype(np.int32)
+    lengths[G - L] = 24                # first chunk of row G-L ...
+    lengths[2 * G - 1 - (G - L)] = 1000   # ... and its second chunk
+    tokens = rng.integers(0, 50, int(lengths.sum())).astype(np.uint8)
+    codec = codecs["lossless"]
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    _set_dec_env(monkeypatch, seg)
+    back, status, tok_off = _decode_direct(codec, words, woff, wcnt, lengths, host_lengths=host)
+    log = capfd.readouterr().err
+    assert f"leftover {L} paired" in log and "steps 1025" in log, log
+    assert not status.any()
+    for i in range(len(lengths)):
+        s = slice(tok_off[i], tok_off[i] + lengths[i])
+        assert np.array_equal(back[s], tokens[s]), i
+
+
 def test_decompress_status_survives_later_segments(codecs, monkeypatch):
     """A corrupt chunk in a workgroup whose rows all end in the first 64-step
     launch keeps its status through the later launches another workgroup's
