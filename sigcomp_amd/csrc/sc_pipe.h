@@ -518,12 +518,13 @@ __device__ __forceinline__ v16i gemm_layer0_position(const v4i *wp, int p, const
 // n-tiles) with side work in its first positions and a hook before the
 // last one:
 //
-//   positions 0 .. 4*ng-1 in ng bodies of four positions (16 k-steps): in
-//     k-step I of body q, side.template piece<I>(q) runs in the same
+//   positions 0 .. 4*SP*ng-1 in ng bodies of 4*SP positions (16*SP
+//     k-steps): in body k-step SP*I of body q, side.template piece<I>(q)
+//     (I = 0..15) runs in the same
 //     scheduling region as the k-step's MFMAs (instruction groups of one
 //     MFMA and XV other VALU), then side.template after<I>(q) (the side
 //     work's rare paths: wave-uniform branches between regions);
-//   positions 4*ng .. 62 plain;
+//   positions 4*SP*ng .. 62 plain;
 //   mid() (the caller's barrier that publishes step t's symbols);
 //   position 63, its table addresses read after mid().
 //
@@ -547,7 +548,7 @@ __device__ __forceinline__ void kstep_schedule_side() {
     });
 }
 
-template <int NTP, int RT, int XV, class AposFn, class NtFn, class AccFn, class InitFn, class Side, class Mid>
+template <int NTP, int RT, int XV, int SP, class AposFn, class NtFn, class AccFn, class InitFn, class Side, class Mid>
 __device__ __forceinline__ void gemm_layer0_ov(const WStream &ws, NtFn nt, const uint8_t *s_emb, AposFn apos,
                                                AccFn acc, InitFn init, int lane, int ng, Side &side, Mid &&mid) {
     constexpr int PD = 4;
@@ -614,12 +615,17 @@ __device__ __forceinline__ void gemm_layer0_ov(const WStream &ws, NtFn nt, const
     };
     using F = std::false_type;
     using T = std::true_type;
-    // position p (parity H): its next position's addresses first
-    auto position = [&](int p, int q, auto hc, auto firstc, auto piece0c, auto nextbc) __attribute__((always_inline)) {
-        constexpr int h = decltype(hc)::value, hn = h ^ 1, P0 = decltype(piece0c)::value;
+    // position p (parity H): its next position's addresses first.  B0: the
+    // body k-step index of its first k-step (-1: no side work); body k-step
+    // b carries side piece b / SP when SP divides it
+    auto position = [&](int p, int q, auto hc, auto firstc, auto b0c, auto nextbc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value, hn = h ^ 1, B0 = decltype(b0c)::value;
 #pragma unroll
         for (int i = 0; i < RT; ++i) ea[hn][i] = an[hn][i] + kg;
-        auto pc = [](auto sc) { return std::integral_constant<int, P0 < 0 ? -1 : P0 + decltype(sc)::value>{}; };
+        auto pc = [](auto sc) {
+            constexpr int b = B0 + decltype(sc)::value;
+            return std::integral_constant<int, B0 < 0 || b % SP != 0 ? -1 : b / SP>{};
+        };
         kstep(p, q, hc, std::integral_constant<int, 0>{}, firstc, pc(std::integral_constant<int, 0>{}), T{});
         kstep(p, q, hc, std::integral_constant<int, 1>{}, F{}, pc(std::integral_constant<int, 1>{}), T{});
         kstep(p, q, hc, std::integral_constant<int, 2>{}, F{}, pc(std::integral_constant<int, 2>{}), T{});
@@ -628,20 +634,22 @@ __device__ __forceinline__ void gemm_layer0_ov(const WStream &ws, NtFn nt, const
     using H0 = std::integral_constant<int, 0>;
     using H1 = std::integral_constant<int, 1>;
     using NP = std::integral_constant<int, -1>;
-    // a body: four positions with side pieces 0..15
+    // a body: 4 * SP positions with side pieces 0..15
     auto body = [&](int q, auto firstc) __attribute__((always_inline)) {
-        const int p0 = 4 * q;
-        position(p0, q, H0{}, firstc, std::integral_constant<int, 0>{}, T{});
-        position(p0 + 1, q, H1{}, F{}, std::integral_constant<int, 4>{}, T{});
-        position(p0 + 2, q, H0{}, F{}, std::integral_constant<int, 8>{}, T{});
-        position(p0 + 3, q, H1{}, F{}, std::integral_constant<int, 12>{}, T{});
+        const int p0 = 4 * SP * q;
+        static_for<4 * SP>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int pp = decltype(pc)::value;
+            using HP = std::integral_constant<int, pp & 1>;
+            using FP = std::integral_constant<bool, decltype(firstc)::value && pp == 0>;
+            position(p0 + pp, q, HP{}, FP{}, std::integral_constant<int, 4 * pp>{}, T{});
+        });
     };
     int pbeg = 0;
     if (ng > 0) {
         body(0, T{});
 #pragma unroll 1
         for (int q = 1; q < ng; ++q) body(q, F{});
-        pbeg = 4 * ng;
+        pbeg = 4 * SP * ng;
     } else {
         position(0, 0, H0{}, T{}, NP{}, T{});
         position(1, 0, H1{}, F{}, NP{}, T{});
@@ -672,7 +680,7 @@ __device__ __forceinline__ void gemm_layer0_ov(const WStream &ws, NtFn nt, const
 // beside it (gemm_layer0_ov): accA / accB receive both passes' layer-0
 // accumulators (bias included), pr the first hidden layer's pass-0
 // parameter block (pipe_rest stores it).
-template <int RT, bool UNI, int XV, class AposFn, class Side, class Mid>
+template <int RT, bool UNI, int XV, int SP, class AposFn, class Side, class Mid>
 __device__ __forceinline__ void pipe_layer0_ov(const ModelDev &M, const uint8_t *s_emb, const uint32_t *s_par,
                                                AposFn apos, v16i (&accA)[PNT][RT], v16i (&accB)[PNT][RT],
                                                uint32_t (&pr)[Slot<UNI>::LANE], int wave, int lane, int ng,
@@ -685,7 +693,7 @@ __device__ __forceinline__ void pipe_layer0_ov(const ModelDev &M, const uint8_t 
     par_fetch<UNI>(M.layer[1].par, nb0, lane, pr);
     const LayerDev &L0 = M.layer[0];
     const WStream ws = make_wstream(L0.w, L0.bytes);
-    gemm_layer0_ov<2 * PNT, RT, XV>(
+    gemm_layer0_ov<2 * PNT, RT, XV, SP>(
         ws, [&](int j) { return j < PNT ? nb0 + j : nb1 + j - PNT; }, s_emb, apos,
         [&](int j, int i) -> v16i & { return j < PNT ? accA[j][i] : accB[j - PNT][i]; },
         [&](int j, int) { return j < PNT ? bias_tile<UNI>(p00, j, g) : bias_tile<UNI>(p10, j - PNT, g); }, lane, ng,
