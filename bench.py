@@ -205,6 +205,20 @@ def split_roofline(model, lengths, seconds, n_cu):
             "algorithmic": f"{per_cu} weight bytes per CU per step x {steps} steps, {groups * p} CUs active"}
 
 
+def calibration_copy(dev, copy_mib):
+    """One plain elementwise kernel moving a known number of bytes (read
+    copy_mib MiB, write copy_mib MiB), outside any timed region: the
+    reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+    if not copy_mib:
+        return
+    import torch
+    src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
     """One configuration's GPU compress + decompress, timed with HIP events on
     its own stream; every chunk round-trips, 24 random chunks' bytes are
@@ -253,15 +267,7 @@ def run_codec(name, steps, warmup, sampler, n_reads=None, e2e=True, copy_mib=0):
                                           _hip.ptr(dstatus), o_len_host.ctypes.data, _hip.ptr(dws),
                                           dws.numel(), stream.cuda_stream))
 
-    if copy_mib:
-        # one plain elementwise kernel moving a known number of bytes (read
-        # copy_mib MiB, write copy_mib MiB), outside the timed region: the
-        # reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters
-        src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+    calibration_copy(dev, copy_mib)
     with torch.cuda.device(dev), torch.cuda.stream(stream):
         for w in range(warmup):
             compress(); decompress()
@@ -519,7 +525,7 @@ def _time_mlp(hm, ctx_d, steps, warmup, sampler):
     return e0.elapsed_time(e1) / 1e3 / steps, (sampler.window(t0, t1) if sampler else None), out
 
 
-def run_mlp(rows, steps, warmup, sampler):
+def run_mlp(rows, steps, warmup, sampler, copy_mib=0):
     """Config c2: `rows` context rows -> int32 CDF tables, seeded random
     per-channel model with the bundled checkpoints' layer dims; 256 random
     rows checked against the oracle.  Beside it, the same rows through the
@@ -540,6 +546,7 @@ def run_mlp(rows, steps, warmup, sampler):
     idx = starts[:, None] + np.arange(64)[None, :]
     ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
     ctx_d = torch.from_numpy(ctx).cuda()
+    calibration_copy(ctx_d.device, copy_mib)
 
     def check(model, out, n, seed):
         sub = np.random.default_rng(seed).choice(rows, n, replace=False)
@@ -568,7 +575,8 @@ def run_mlp(rows, steps, warmup, sampler):
             "power": ({**pw, "j_per_mrow": round(pw["avg_w"] * t / (rows / 1e6), 3)} if pw else None),
             "roofline": {"kernel": "k_mlp_context<cdf>", "bound": "mfma", "achieved": round(achieved, 2),
                          "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                         "traffic": None,
+                         "traffic": pmc_traffic("c2", "k_mlp_context"),
+                         "traffic_source": "profiles/traffic_c2.txt (rocprofv3 PMC, bytes per launch)",
                          "algorithmic": f"{OPS_PER_ROW} int8 ops per row x {rows} rows per launch",
                          **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")},
             "same_rows_other_models": {**side, "note": "the same rows and kernel with a random per-tensor model "
@@ -576,7 +584,7 @@ def run_mlp(rows, steps, warmup, sampler):
 
 
 def bench_mlp(args):
-    r = run_mlp(args.rows, args.steps, args.warmup, None)
+    r = run_mlp(args.rows, args.steps, args.warmup, None, copy_mib=args.copy_mib)
     return {"metric": "INT8 MLP rows/s -> int32 CDF (c2 microbench)", "value": r["mrows_s"], "unit": "Mrows/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
