@@ -39,9 +39,12 @@ constexpr int EMB_BYTES = EMB_ROWS * EMB_STRIDE;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Requant parameters of one 32-output n-tile, 72 dwords: bias[32] (int32),
-// m0[32] (uint32), shift[32] (uint8, packed four per dword).
-constexpr int PAR_DWORDS = 72;
+// Requant parameters of one 32-output n-tile, 104 dwords: bias[32] (int32),
+// m0[32] (uint32), shift[32] (uint8, packed four per dword), then for
+// layers on the 32-bit path (LayerDev::fast) hi[32] (int32): each output's
+// pre-shift clamp bound min(128 * 2**shift - 1, 2**31 - 1), shift - 32 as
+// stored (the per-channel form of LayerDev::uhi).
+constexpr int PAR_DWORDS = 104;
 constexpr int PAR_LDS_DWORDS = 4 * PAR_DWORDS * 4;   // 4 waves x up to 4 n-tiles
 
 struct LayerDev {

@@ -629,7 +629,8 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
         // (the same product); layers whose every m0 < 2**31 and shift >= 32
         // take the 32-bit high-product path (requant_u8_fast), with
         // shift - 32 stored.  Packed per 32-output n-tile: bias[32], m0[32],
-        // shift[32] (bytes), PAR_DWORDS dwords per n-tile.
+        // shift[32] (bytes), and for those layers the pre-shift clamp
+        // bounds hi[32]; PAR_DWORDS dwords per n-tile.
         std::vector<uint32_t> m0(L.n);
         std::vector<uint8_t> sh(L.n);
         bool fast = true;
@@ -666,6 +667,7 @@ int sc_model_create(const int8_t *emb, int32_t emb_rows, int32_t emb_dim, int32_
                 blk[x] = (uint32_t)L.bias[j];
                 blk[32 + x] = m0[j];
                 blk[64 + x / 4] |= (uint32_t)sh[j] << (8 * (x % 4));
+                if (fast) blk[72 + x] = (uint32_t)std::min<int64_t>((int64_t(128) << sh[j]) - 1, INT32_MAX);
             }
         }
         rc = upload(m, par, &D.par);

@@ -23,8 +23,9 @@
 //
 // With UNI (CORE_PIPE_UNI: per-tensor constants on every layer) every
 // requantisation is rq_words_uni / rq_pass_uni and the parameter slots hold
-// only biases; else the hidden layers use rq_word, layer 0's first pass and
-// the output layer requant_pack_t.
+// only biases; else the parameter slots hold whole parameter blocks and the
+// requantisation is rq_word / rq_pass_pc (per-channel constants, the same
+// four instructions per value).
 // Requires every layer to take the 32-bit requant path (LayerDev::fast), ReLU
 // on all layers but the last, and 512-wide hidden layers (ModelDev::pipe).
 #pragma once
@@ -80,11 +81,11 @@ __device__ __forceinline__ v16i bias_tile(const uint32_t *blk, int j, int g) {
     return t;
 }
 
-// Requant parameters (M0 and shift; the bias is already in the accumulators)
-// of packed group g of n-tile j (lane half g2).
+// Requant parameters (M0, clamp bounds and shifts; the bias is already in
+// the accumulators) of packed group g of n-tile j (lane half g2).
 struct RqPar {
-    v4i mm;
-    uint32_t sh;
+    v4i mm, hi;
+    uint32_t sh;   // four shifts - 32, one byte each
 };
 
 __device__ __forceinline__ RqPar rq_par(const uint32_t *blk, int j, int g, int g2) {
@@ -92,22 +93,74 @@ __device__ __forceinline__ RqPar rq_par(const uint32_t *blk, int j, int g, int g
     const int o = 8 * g + 4 * g2;
     RqPar p;
     p.mm = *(const v4i *)(pj + 32 + o);
+    p.hi = *(const v4i *)(pj + 72 + o);
     p.sh = pj[64 + (o >> 2)];
     return p;
 }
 
+// Byte E of `packed` = y >> (byte E of sh): the shift amount is read out of
+// the packed shifts by the SDWA source select, the result written into its
+// byte by the destination select (byte 0 clears the others).  Logical shift
+// after a ReLU clamp (y >= 0), else arithmetic.
+template <bool RELU, int E>
+__device__ __forceinline__ void rq_insert_pc(uint32_t &packed, uint32_t sh, int y) {
+#define SC_RQ_INS(OP, B, U, C)                                                                               \
+    asm(OP "_sdwa %0, %1, %2 dst_sel:BYTE_" #B " dst_unused:" U " src0_sel:BYTE_" #B " src1_sel:DWORD" \
+        : C(packed) : "v"(sh), "v"(y))
+    if constexpr (RELU) {
+        if constexpr (E == 0) SC_RQ_INS("v_lshrrev_b32", 0, "UNUSED_PAD", "=v");
+        else if constexpr (E == 1) SC_RQ_INS("v_lshrrev_b32", 1, "UNUSED_PRESERVE", "+v");
+        else if constexpr (E == 2) SC_RQ_INS("v_lshrrev_b32", 2, "UNUSED_PRESERVE", "+v");
+        else SC_RQ_INS("v_lshrrev_b32", 3, "UNUSED_PRESERVE", "+v");
+    } else {
+        if constexpr (E == 0) SC_RQ_INS("v_ashrrev_i32", 0, "UNUSED_PAD", "=v");
+        else if constexpr (E == 1) SC_RQ_INS("v_ashrrev_i32", 1, "UNUSED_PRESERVE", "+v");
+        else if constexpr (E == 2) SC_RQ_INS("v_ashrrev_i32", 2, "UNUSED_PRESERVE", "+v");
+        else SC_RQ_INS("v_ashrrev_i32", 3, "UNUSED_PRESERVE", "+v");
+    }
+#undef SC_RQ_INS
+}
+
 // Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile (bias included)
-// -> packed int8.
+// -> packed int8, per-channel constants of a layer on the 32-bit path: x =
+// hi32(a * m0) clamped to [lo, hi] before the shift (lo = 0 with ReLU, else
+// -hi - 1 = max(-128 * 2**shift, -2**31)), as the per-tensor form below
+// argues; four VALU instructions per value with the accumulator read.
 template <bool RELU>
 __device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar &p) {
-    constexpr int lo = RELU ? 0 : -128;
-    uint32_t packed = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t q = requant_u8_fast(acc[4 * g + e], 0, p.mm[e], (p.sh >> (8 * e)) & 63u, lo);
-        packed |= q << (8 * e);
-    }
+    uint32_t packed;
+    static_for<4>([&](auto ec) __attribute__((always_inline)) {
+        constexpr int e = decltype(ec)::value;
+        const int x = __mulhi(acc[4 * g + e], p.mm[e]), hi = p.hi[e];
+        int y;
+        if constexpr (RELU) {
+            asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y) : "v"(x), "v"(hi));
+        } else {
+            const int lo = ~hi;
+            asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(x), "v"(lo), "v"(hi));
+        }
+        rq_insert_pc<RELU, e>(packed, p.sh, y);
+    });
     return packed;
+}
+
+// All n-tiles and row tiles of a pass, per-channel constants from the LDS
+// parameter blocks at `blk` (the requantisations not interleaved with MFMAs).
+template <bool RELU, int RT>
+__device__ __forceinline__ void rq_pass_pc(const v16i (&acc)[PNT][RT], const uint32_t *blk, int lane,
+                                           uint32_t (&pk)[PNT][RT][4]) {
+    const int g2 = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < PNT; ++j)
+        static_for<4>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value;
+            const RqPar p = rq_par(blk, j, g, g2);
+#pragma unroll
+            for (int i = 0; i < RT; ++i) {
+                pk[j][i][g] = rq_word<RELU>(acc[j][i], g, p);
+                asm volatile("" : "+v"(pk[j][i][g]));
+            }
+        });
 }
 
 // Per-tensor constants (LayerDev::uni): x = hi32(a * m0) is clamped to
@@ -394,7 +447,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
             for (int i = 0; i < RT; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[set][slot][j], b[kt & 1][i],
                                                                   kt == 0 ? bias[j] : acc[j][i], 0, 0, 0);
-        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + (UNI ? 0 : 2) + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
+        pipe_schedule<MF, (v != 7 && v != NV - 1 ? RT : 0) + (UNI ? 0 : 3) + (v == KTH - 1 ? 4 * PNT : 0), PNT, VA>();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (v == 7) {
             // layer l-1 pass 1 -> region B; this layer's pass-1 and the next
@@ -411,7 +464,7 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     });
     if constexpr (LASTL) {
         if constexpr (UNI) rq_pass_uni<false, RT>(accA, rq_uni(L), pk);
-        else requant_pack_t<PNT, RT, true, false, false>(accA, cur0, lane, pk);
+        else rq_pass_pc<false, RT>(accA, cur0, lane, pk);
         __syncthreads();
         pstore_natural<RT>(pk, nb0, s_act, lane);
     } else {
@@ -719,7 +772,7 @@ __device__ __forceinline__ void pipe_rest(const ModelDev &M, uint8_t *s_act, uin
         const LayerDev &L0 = M.layer[0];
         par_put<UNI>(s_parw + slot_p0(1) * BLK, pr, lane);
         if constexpr (UNI) rq_pass_uni<true, RT>(accA, rq_uni(L0), pk);
-        else requant_pack_t<PNT, RT, true, true, false>(accA, s_parw + slot_p0(0) * BLK, lane, pk);
+        else rq_pass_pc<true, RT>(accA, s_parw + slot_p0(0) * BLK, lane, pk);
         pstore_perm<RT>(pk, nb0, s_act, lane);
         const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
 #pragma unroll
@@ -782,7 +835,7 @@ __device__ __forceinline__ void mlp_rows_pipe(const ModelDev &M, const uint8_t *
             [&](int j, int) { return bias[j]; }, lane);
         par_put<UNI>(s_parw + slot_p0(1) * BLK, prn, lane);
         if constexpr (UNI) rq_pass_uni<true, RT>(accA, rq_uni(L0), pk);
-        else requant_pack_t<PNT, RT, true, true, false>(accA, p00, lane, pk);
+        else rq_pass_pc<true, RT>(accA, p00, lane, pk);
         pstore_perm<RT>(pk, nb0, s_act, lane);
         const __amdgpu_buffer_rsrc_t rs1 = layer_rsrc(M.layer[1]);
 #pragma unroll
