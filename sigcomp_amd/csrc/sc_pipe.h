@@ -24,8 +24,8 @@
 // With UNI (CORE_PIPE_UNI: per-tensor constants on every layer) every
 // requantisation is rq_words_uni / rq_pass_uni and the parameter slots hold
 // only biases; else the parameter slots hold whole parameter blocks and the
-// requantisation is rq_word / rq_pass_pc (per-channel constants, the same
-// four instructions per value).
+// requantisation is rq_bytes_pc / rq_pass_pc (per-channel constants, the
+// same four instructions per value).
 // Requires every layer to take the 32-bit requant path (LayerDev::fast), ReLU
 // on all layers but the last, and 512-wide hidden layers (ModelDev::pipe).
 #pragma once
@@ -121,27 +121,33 @@ __device__ __forceinline__ void rq_insert_pc(uint32_t &packed, uint32_t sh, int 
 #undef SC_RQ_INS
 }
 
-// Features 8g + 4*g2 + e (e = 0..3) of one accumulator tile (bias included)
-// -> packed int8, per-channel constants of a layer on the 32-bit path: x =
-// hi32(a * m0) clamped to [lo, hi] before the shift (lo = 0 with ReLU, else
-// -hi - 1 = max(-128 * 2**shift, -2**31)), as the per-tensor form below
-// argues; four VALU instructions per value with the accumulator read.
-template <bool RELU>
-__device__ __forceinline__ uint32_t rq_word(const v16i &acc, int g, const RqPar &p) {
-    uint32_t packed;
-    static_for<4>([&](auto ec) __attribute__((always_inline)) {
-        constexpr int e = decltype(ec)::value;
-        const int x = __mulhi(acc[4 * g + e], p.mm[e]), hi = p.hi[e];
-        int y;
-        if constexpr (RELU) {
-            asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y) : "v"(x), "v"(hi));
-        } else {
-            const int lo = ~hi;
-            asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(x), "v"(lo), "v"(hi));
+// Bytes E0 <= e < E1 of every row tile's word pk[i][g] (features 8g +
+// 4*g2 + e, bias included in the accumulators), per-channel constants of a
+// layer on the 32-bit path: x = hi32(a * m0) clamped to [lo, hi] before the
+// shift (lo = 0 with ReLU, else -hi - 1 = max(-128 * 2**shift, -2**31)), as
+// the per-tensor form below argues; four VALU instructions per value with
+// the accumulator read.  The inserts run across the row tiles' words; the
+// first byte's (e = 0) clears the rest of its word, so E0 = 0 comes first.
+template <bool RELU, int E0, int E1, int RT>
+__device__ __forceinline__ void rq_bytes_pc(const v16i (&acc)[RT], int g, const RqPar &p, uint32_t (&pk)[RT][4]) {
+    int y[4][RT];
+#pragma unroll
+    for (int e = E0; e < E1; ++e)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            const int x = __mulhi(acc[i][4 * g + e], p.mm[e]), hi = p.hi[e];
+            if constexpr (RELU) {
+                asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y[e][i]) : "v"(x), "v"(hi));
+            } else {
+                const int lo = ~hi;
+                asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y[e][i]) : "v"(x), "v"(lo), "v"(hi));
+            }
         }
-        rq_insert_pc<RELU, e>(packed, p.sh, y);
+    static_for<E1 - E0>([&](auto ec) __attribute__((always_inline)) {
+        constexpr int e = E0 + decltype(ec)::value;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) rq_insert_pc<RELU, e>(pk[i][g], p.sh, y[e][i]);
     });
-    return packed;
 }
 
 // All n-tiles and row tiles of a pass, per-channel constants from the LDS
@@ -154,19 +160,16 @@ __device__ __forceinline__ void rq_pass_pc(const v16i (&acc)[PNT][RT], const uin
     for (int j = 0; j < PNT; ++j)
         static_for<4>([&](auto gc) __attribute__((always_inline)) {
             constexpr int g = decltype(gc)::value;
-            const RqPar p = rq_par(blk, j, g, g2);
+            rq_bytes_pc<RELU, 0, 4, RT>(acc[j], g, rq_par(blk, j, g, g2), pk[j]);
 #pragma unroll
-            for (int i = 0; i < RT; ++i) {
-                pk[j][i][g] = rq_word<RELU>(acc[j][i], g, p);
-                asm volatile("" : "+v"(pk[j][i][g]));
-            }
+            for (int i = 0; i < RT; ++i) asm volatile("" : "+v"(pk[j][i][g]));
         });
 }
 
 // Per-tensor constants (LayerDev::uni): x = hi32(a * m0) is clamped to
 // [0, uhi] BEFORE the shift, uhi = 128 * 2**sh - 1 (or 2**31 - 1 when that
 // overflows; then x >> sh < 128 anyway).  floor(x / 2**sh) is monotone in
-// x, so this equals min(max(x >> sh, 0), 127) of rq_word<true>; the shift
+// x, so this equals min(max(x >> sh, 0), 127) of requant_u8_fast; the shift
 // then writes each byte straight into the packed word (SDWA destination
 // select; byte 0 clears the others).  Four VALU instructions per value with
 // the accumulator read, and no per-channel operands.
@@ -229,6 +232,29 @@ __device__ __forceinline__ void rq_words_uni(const v16i (&acc)[RT], int g, const
         constexpr int e = decltype(ec)::value;
 #pragma unroll
         for (int i = I0; i < I1; ++i) rq_insert_uni<RELU, e>(pk[i][g], p.sh, y[e][i]);
+    });
+}
+// Bytes E0 <= e < E1 of every row tile's word pk[i][g] (features
+// 8g + 4*g2 + e), the inserts running across the row tiles' words.  The
+// first byte's insert (e = 0) clears the rest of its word, so E0 = 0 comes
+// first.
+template <bool RELU, int E0, int E1, int RT>
+__device__ __forceinline__ void rq_bytes_uni(const v16i (&acc)[RT], int g, const RqUni &p, uint32_t (&pk)[RT][4]) {
+    int y[4][RT];
+#pragma unroll
+    for (int e = E0; e < E1; ++e)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            if constexpr (RELU)
+                asm("v_med3_i32 %0, %1, 0, %2" : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "s"(p.hi));
+            else
+                asm("v_med3_i32 %0, %1, %2, %3"
+                    : "=v"(y[e][i]) : "v"(__mulhi(acc[i][4 * g + e], p.m0)), "v"(p.lo), "s"(p.hi));
+        }
+    static_for<E1 - E0>([&](auto ec) __attribute__((always_inline)) {
+        constexpr int e = E0 + decltype(ec)::value;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) rq_insert_uni<RELU, e>(pk[i][g], p.sh, y[e][i]);
     });
 }
 // All n-tiles and row tiles of a pass (the requantisations that are not
@@ -360,7 +386,6 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
     constexpr int PPD = ppd<RT>();
     constexpr int NV = LASTL ? KTH : 2 * KTH;
     constexpr int MF = PNT * RT;
-    constexpr int RH = (RT + 1) / 2;          // row tiles requantised in the first of two steps
     const int g = lane >> 5, voff = lane * 16;
     const int bbase = pact_off(lane & 31, g);
     const __amdgpu_buffer_rsrc_t rs = layer_rsrc(L);
@@ -420,18 +445,16 @@ __device__ __forceinline__ void pipe_hidden(const LayerDev &Lp, const LayerDev &
             } else {
                 const RqPar cur = pp;
                 if constexpr (v + 1 < 8) pp = rq_par(prev1, (v + 1) / 4, (v + 1) % 4, g);
-#pragma unroll
-                for (int i = 0; i < RT; ++i) pk[j][i][gg] = rq_word<true>(accB[j][i], gg, cur);
+                rq_bytes_pc<true, 0, 4, RT>(accB[j], gg, cur, pk[j]);
             }
         } else if constexpr (!LASTL && v >= 16) {
             constexpr int u = v - 16, j = u / 8, gg = (u / 2) % 4, h = u % 2;
             if constexpr (UNI) {
-                rq_words_uni<true, h * RH, (h ? RT : RH)>(accA[j], gg, uc, pk[j]);
+                rq_bytes_uni<true, 2 * h, 2 * h + 2, RT>(accA[j], gg, uc, pk[j]);
             } else {
                 const RqPar cur = pp;
                 if constexpr (u + 1 < 16) pp = rq_par(cur0, (u + 1) / 8, ((u + 1) / 2) % 4, g);
-#pragma unroll
-                for (int i = h * RH; i < (h ? RT : RH); ++i) pk[j][i][gg] = rq_word<true>(accA[j][i], gg, cur);
+                rq_bytes_pc<true, 2 * h, 2 * h + 2, RT>(accA[j], gg, cur, pk[j]);
             }
         }
         // pass 1's bias tiles, one step before its first MFMAs
