@@ -478,10 +478,11 @@ hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
 // Per-step cost of a full-wave decode launch at rt = 1 .. DEC_RT_MAX row
 // tiles per workgroup (MI355X, 512-token chunks, lossless model; us x 10 per
-// step; rt <= 4 runs the pipelined core with per-tensor requantisation).
-// Per row tile rt = 3 and 4 are cheapest (38.5 and 39.0 us), rt = 1 the
-// dearest (66.6 us).
-constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 666, 824, 1156, 1561, 2154};
+// step, one box; rt <= 4 runs the pipelined core with per-tensor
+// requantisation, rt = 2 and 3 with the epilogue beside the next step's
+// layer 0).  Per row tile rt = 4 and 3 are cheapest (34.8 and 35.6 us), rt = 1
+// the dearest (62.1 us).
+constexpr int DEC_STEP_COST[DEC_RT_MAX + 1] = {0, 621, 763, 1067, 1390, 2091};
 // Per-step cost of a split decode launch (at most XCH_MAX_GROUPS groups of
 // 32 chunks) with 4 and 8 workgroups per group, same unit.
 constexpr int DEC_SPLIT_STEP_COST_P4 = 282, DEC_SPLIT_STEP_COST_P8 = 256;
