@@ -848,6 +848,14 @@ def main():
         sys.exit(2)
     runners = {"all": run_all, "c2": bench_mlp, "ceiling": bench_ceiling, "coder": bench_coder}
     print(json.dumps(runners.get(args.config, run_one)(args)), flush=True)
+    # release every model handle and device buffer, and let the device
+    # finish, while the interpreter and the HIP runtime are still whole
+    # (rather than from finalisers during interpreter shutdown)
+    import gc
+    import torch
+    gc.collect()
+    if torch.cuda.is_available():
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":

@@ -229,7 +229,9 @@ int64_t sc_decompress_workspace_bytes(int64_t n_chunks);
  * list_of_lengths is host data): with it the launch plan is computed on the
  * host and the call only enqueues work on `stream`; with NULL the plan's
  * length statistics are computed on the device and read back, so the call
- * waits for the work already queued on `stream`.  Chunks sorted by
+ * waits for the work already queued on `stream`; on a stream under graph
+ * capture that wait is not possible, and lengths_host NULL is SC_ERR_ARG
+ * before anything is enqueued (the capture stays valid).  Chunks sorted by
  * descending length (as QuantMLPCompression passes them) give the shortest
  * schedule: the shortest chunks are then left over after the full waves of
  * workgroups and follow the shortest chunks of the last full wave in the
@@ -247,6 +249,19 @@ int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int
                          const int32_t *lengths_host, void *workspace, int64_t workspace_bytes,
                          void *stream);
 
+/* sc_decompress_chunks with options (a bitwise or of SC_DEC_OPT_*; any other
+ * bit is SC_ERR_ARG).  SC_DEC_OPT_NO_SPLIT: every launch runs unsplit (one
+ * workgroup per 32-chunk tile, no wait between workgroups), as
+ * QuantMLPCompression.decompress_flat re-runs the chunks of a split launch
+ * that reported SC_STATUS_SYNC_TIMEOUT.  Replaces the same reference call
+ * as sc_decompress_chunks (quant_mlp_export.py:325-377). */
+#define SC_DEC_OPT_NO_SPLIT 1
+int sc_decompress_chunks_opts(const sc_model *model, const uint32_t *words, const int64_t *word_off,
+                              const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks,
+                              uint8_t *tokens, const int64_t *tok_off, int32_t *status,
+                              const int32_t *lengths_host, void *workspace, int64_t workspace_bytes,
+                              int32_t options, void *stream);
+
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  sc_decompress_chunks with its workspace replaced by a
@@ -257,7 +272,7 @@ int sc_decompress_chunks(const sc_model *model, const uint32_t *words, const int
  * SC_ERR_ARG.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (on different streams or threads) race.  With
  * lengths_host NULL the call waits for its stream, as sc_decompress_chunks
- * does.  Models of the bundled architecture only (SC_ERR_UNSUPPORTED for a
+ * does (and is SC_ERR_ARG under graph capture).  Models of the bundled architecture only (SC_ERR_UNSUPPORTED for a
  * generic model, whose path allocates scratch memory). */
 #define SC_STATIC_DEC_MAX_CHUNKS 65536
 int sc_decompress_chunks_static(const sc_model *model, const uint32_t *words, const int64_t *word_off,

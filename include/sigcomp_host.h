@@ -195,8 +195,9 @@ int sc_sig2_read_index(const uint8_t *data, int64_t size, int64_t n_expected, in
  * bits, a zero bit and the k low bits of v (low bit first); else MQ one bits
  * and v in FB bits (low bit first).  An empty array is the single byte 0,
  * as _rice_compress writes it (main.py:176-177).
- * Decoding is strict: k > min(FB, 31), a stream that ends early, or any
- * byte or non-zero padding bit after the last value is SC_HOST_ERR_RICE. */
+ * Decoding is strict: k > min(FB, 31), a quotient whose value would not
+ * fit FB bits (q << k >= 2**FB), a stream that ends early, or any byte or
+ * non-zero padding bit after the last value is SC_HOST_ERR_RICE. */
 
 /* Largest blob of n values (bytes). */
 int64_t sc_rice_bound(int64_t n, int32_t fallback_bits, int32_t max_quotient);
@@ -211,7 +212,9 @@ int sc_rice_encode(const uint32_t *vals, const int64_t *off, const int64_t *coun
 
 /* Decode n_items blobs: blob i = blob_len[i] bytes at blobs[i], holding
  * count[i] values, written to out + out_off[i]; a count of 0 reads nothing
- * (_rice_decompress returns an empty array without reading, main.py:184-185). */
+ * (_rice_decompress returns an empty array without reading, main.py:184-185).
+ * A negative count is SC_ERR_ARG (bad = its index), found before any value
+ * is written. */
 int sc_rice_decode(const uint8_t *const *blobs, const int64_t *blob_len, const int64_t *count, int64_t n_items,
                    int32_t fallback_bits, int32_t max_quotient, uint32_t *out, const int64_t *out_off,
                    int32_t n_threads, int64_t *bad);

@@ -16,6 +16,9 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libsigcomp_hip.so"
 
 SC_OK = 0
+SC_ERR_ARG = 1
+SC_ERR_HIP = 2
+SC_ERR_UNSUPPORTED = 3
 SC_STATUS_OK = 0
 SC_STATUS_CAPACITY = 1
 SC_STATUS_INVALID_STREAM = 2
@@ -27,9 +30,13 @@ EXPORTED = (
     "sc_model_core",
     "sc_mlp_forward", "sc_mlp_forward_cdf", "sc_logits_to_cdf", "sc_encode_step",
     "sc_encode_seal", "sc_decode_step", "sc_compress_workspace_bytes", "sc_compress_chunks",
-    "sc_decompress_workspace_bytes", "sc_decompress_chunks", "sc_decompress_chunks_static",
+    "sc_decompress_workspace_bytes", "sc_decompress_chunks", "sc_decompress_chunks_opts",
+    "sc_decompress_chunks_static",
     "sc_gather_words", "sc_mfma_burn_i8",
 )
+
+# sc_decompress_chunks_opts options
+SC_DEC_OPT_NO_SPLIT = 1
 
 # chunks per sc_decompress_chunks_static call (SC_STATIC_DEC_MAX_CHUNKS)
 STATIC_DEC_MAX_CHUNKS = 65536
@@ -95,6 +102,7 @@ def lib():
         L.sc_decompress_workspace_bytes.argtypes = [_I64]
         L.sc_decompress_workspace_bytes.restype = _I64
         L.sc_decompress_chunks.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P]
+        L.sc_decompress_chunks_opts.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I32, _P]
         L.sc_decompress_chunks_static.argtypes = [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P]
         L.sc_gather_words.argtypes = [_P, _P, _P, _I64, _P, _P, _P]
         L.sc_mfma_burn_i8.argtypes = [_P, _I32, _I32, _P, _P]

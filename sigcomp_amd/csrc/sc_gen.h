@@ -11,7 +11,8 @@
 namespace sc {
 
 constexpr int R_GEN_TILE = R_TILE;              // steps per compress tile descriptor (k_tile_table)
-constexpr int64_t GEN_BATCH_ROWS = 1 << 16;     // rows per launch batch (bounds the scratch memory)
+constexpr int64_t GEN_BATCH_ROWS = 1 << 16;     // rows per launch batch at most
+constexpr int64_t GEN_SCRATCH_BYTES = 1 << 30;  // scratch per call at most (batches shrink for wide models)
 
 // Scratch memory of these calls comes from hipMallocAsync / hipFreeAsync on
 // the call's stream.  Return SC_OK or SC_ERR_HIP with `err` set.

@@ -262,6 +262,18 @@ int64_t max_width(const ModelDev &M) {
     return w;
 }
 
+// Rows per batch of a call that needs `needed` rows: at most
+// GEN_BATCH_ROWS, at most what GEN_SCRATCH_BYTES holds at this model's width
+// (two activation buffers and the logits per row), and no more than the
+// call needs; a multiple of `unit` (64-row MLP tiles, 128-step compress
+// tiles).  The widest model sc_model_create accepts (2**20 inputs) still
+// gets 384 rows.
+int64_t batch_rows(const ModelDev &M, int64_t needed, int64_t unit) {
+    const int64_t per_row = 2 * max_width(M) + VOCAB;
+    const int64_t fit = std::max<int64_t>(GEN_SCRATCH_BYTES / per_row / unit, 1) * unit;
+    return std::min({GEN_BATCH_ROWS / unit * unit, fit, round_up(std::max<int64_t>(needed, 1), unit)});
+}
+
 hipError_t launch_check() { return hipGetLastError(); }
 
 // Stream-ordered scratch of one call (hipMallocAsync / hipFreeAsync).
@@ -307,8 +319,8 @@ hipError_t gen_mlp(const ModelDev &M, const GenRows &g, int64_t rows, int8_t *X0
 
 int gen_mlp_forward(const ModelDev &M, const int64_t *ctx, int64_t rows, int8_t *logits, int32_t *cdf,
                     int32_t *status, hipStream_t s, std::string &err) {
-    const int64_t B = std::min<int64_t>(rows, GEN_BATCH_ROWS);
-    const int64_t width = max_width(M), rows_p = round_up(B, 64);
+    const int64_t B = batch_rows(M, rows, 64);
+    const int64_t width = max_width(M), rows_p = B;
     Scratch scr(s);
     hipError_t e = scr.alloc((size_t)(2 * rows_p * width + (cdf ? rows_p * VOCAB : 0)));
     if (e != hipSuccess) {
@@ -336,8 +348,8 @@ int gen_mlp_forward(const ModelDev &M, const int64_t *ctx, int64_t rows, int8_t 
 
 int gen_compress(const ModelDev &M, const uint8_t *tokens, const int32_t *tile_start, int64_t n_chunks,
                  const int4 *desc, int64_t max_tiles, uint2 *pairs, hipStream_t s, std::string &err) {
-    const int64_t tiles_per = GEN_BATCH_ROWS / R_GEN_TILE;
-    const int64_t rows_b = tiles_per * R_GEN_TILE, width = max_width(M);
+    const int64_t rows_b = batch_rows(M, max_tiles * R_GEN_TILE, R_GEN_TILE), width = max_width(M);
+    const int64_t tiles_per = rows_b / R_GEN_TILE;
     Scratch scr(s);
     hipError_t e = scr.alloc((size_t)(2 * rows_b * width + rows_b * VOCAB));
     if (e != hipSuccess) {
@@ -365,7 +377,7 @@ int gen_decompress(const ModelDev &M, const uint32_t *words, const int64_t *word
                    const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
                    int32_t *status, DecState *state, int32_t max_len, hipStream_t s, std::string &err) {
     const int64_t width = max_width(M);
-    const int64_t B = std::min<int64_t>(n_chunks, GEN_BATCH_ROWS), rows_p = round_up(B, 64);
+    const int64_t B = batch_rows(M, n_chunks, 64), rows_p = B;
     Scratch scr(s);
     hipError_t e = scr.alloc((size_t)(2 * rows_p * width + rows_p * VOCAB));
     if (e != hipSuccess) {
@@ -373,7 +385,7 @@ int gen_decompress(const ModelDev &M, const uint32_t *words, const int64_t *word
         return SC_ERR_HIP;
     }
     int8_t *X0 = (int8_t *)scr.p, *X1 = X0 + rows_p * width, *lg = X1 + rows_p * width;
-    // groups of at most GEN_BATCH_ROWS chunks, each decoded step by step
+    // groups of at most B chunks, each decoded step by step
     for (int64_t c0 = 0; c0 < n_chunks && e == hipSuccess; c0 += B) {
         const int64_t n = std::min(B, n_chunks - c0);
         hipLaunchKernelGGL(k_gen_dec_init, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, words, word_off + c0,

@@ -716,14 +716,20 @@ int sc_rice_decode(const uint8_t *const *blobs, const int64_t *blob_len, const i
         g_err = "bad argument";
         return SC_ERR_ARG;
     }
+    // every count is checked before anything is written: the output
+    // offsets of the items after a negative count would not be valid
+    for (int64_t i = 0; i < n_items; ++i)
+        if (count[i] < 0) {
+            if (bad) *bad = i;
+            g_err = "negative value count";
+            return SC_ERR_ARG;
+        }
     FirstBad fb;
     const int kmax = rice_kmax(fallback_bits);
+    const uint64_t lim = fallback_bits == 32 ? 0x100000000ull : (1ull << fallback_bits);
     parallel_for(n_items, n_threads, [&](int64_t i) {
         const int64_t n = count[i];
-        if (n <= 0) {
-            if (n < 0) fb.report(i, SC_ERR_ARG);
-            return;
-        }
+        if (n == 0) return;
         const uint8_t *b = blobs[i];
         const int64_t len = blob_len[i];
         if (len < 2 || !b || b[0] > kmax) {
@@ -745,7 +751,7 @@ int sc_rice_decode(const uint8_t *const *blobs, const int64_t *blob_len, const i
                     fb.report(i, SC_HOST_ERR_RICE);
                     return;
                 }
-                if (((uint64_t)q << k) > 0xFFFFFFFFull) {   // no value of 32 bits has this quotient
+                if (((uint64_t)q << k) >= lim) {   // no value of the fallback width has this quotient
                     fb.report(i, SC_HOST_ERR_RICE);
                     return;
                 }

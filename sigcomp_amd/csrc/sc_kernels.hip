@@ -896,7 +896,15 @@ static void host_len_stats(const int32_t *len, int64_t n, int64_t g0, int64_t G,
 static int decompress_run(const sc_model *m, const uint32_t *words, const int64_t *word_off, const int32_t *word_cnt,
                           const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
                           int32_t *status, const int32_t *lengths_host, DecState *state, int32_t *stat_dev,
-                          uint8_t *xch, int64_t xch_groups, hipStream_t s) {
+                          uint8_t *xch, int64_t xch_groups, int32_t options, hipStream_t s) {
+    // Under graph capture nothing may wait for the device: the launch plan
+    // then needs the caller's host copy of the lengths, checked before
+    // anything is enqueued so that a refused call leaves the capture valid.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    SC_HIP(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+    if (capture != hipStreamCaptureStatusNone && !lengths_host)
+        return fail(SC_ERR_ARG, "lengths_host required on a stream under graph capture (the launch plan "
+                                "would read the lengths back from the device)");
     if (m->dev.pipe == CORE_GENERIC) {
         // step by step over all chunks: the longest chunk bounds the steps
         int32_t st4[4];
@@ -974,10 +982,8 @@ static int decompress_run(const sc_model *m, const uint32_t *words, const int64_
     const int split_force = split_env ? atoi(split_env) : -1;
     // (a stream under graph capture gets the unsplit launches: the split
     // one is a cooperative launch)
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    SC_HIP(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
-    const bool split_ok =
-        m->dev.pipe == CORE_PIPE_UNI && xch && split_force != 0 && capture == hipStreamCaptureStatusNone;
+    const bool split_ok = m->dev.pipe == CORE_PIPE_UNI && xch && split_force != 0 &&
+                          !(options & SC_DEC_OPT_NO_SPLIT) && capture == hipStreamCaptureStatusNone;
     // polls before a wait for the peers gives up (SC_HIP_DEC_SPIN: a lower
     // limit, to test the timeout path)
     const char *spin_env = getenv("SC_HIP_DEC_SPIN");
@@ -1076,7 +1082,15 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
                          const int32_t *lengths, int64_t n_chunks, uint8_t *tokens, const int64_t *tok_off,
                          int32_t *status, const int32_t *lengths_host, void *workspace, int64_t workspace_bytes,
                          void *stream) {
-    if (!m || n_chunks < 0) return fail(SC_ERR_ARG, "bad argument");
+    return sc_decompress_chunks_opts(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status,
+                                     lengths_host, workspace, workspace_bytes, 0, stream);
+}
+
+int sc_decompress_chunks_opts(const sc_model *m, const uint32_t *words, const int64_t *word_off,
+                              const int32_t *word_cnt, const int32_t *lengths, int64_t n_chunks, uint8_t *tokens,
+                              const int64_t *tok_off, int32_t *status, const int32_t *lengths_host, void *workspace,
+                              int64_t workspace_bytes, int32_t options, void *stream) {
+    if (!m || n_chunks < 0 || (options & ~SC_DEC_OPT_NO_SPLIT)) return fail(SC_ERR_ARG, "bad argument");
     if (n_chunks == 0) return SC_OK;
     if (!words || !word_off || !word_cnt || !lengths || !tokens || !tok_off || !status || !workspace)
         return fail(SC_ERR_ARG, "null device pointer");
@@ -1086,7 +1100,7 @@ int sc_decompress_chunks(const sc_model *m, const uint32_t *words, const int64_t
     int32_t *stat_dev = (int32_t *)((char *)workspace + dec_state_bytes(n_chunks));
     uint8_t *xch = (uint8_t *)workspace + dec_state_bytes(n_chunks) + 256;
     return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
-                          state, stat_dev, xch, dec_xch_groups(n_chunks), as_stream(stream));
+                          state, stat_dev, xch, dec_xch_groups(n_chunks), options, as_stream(stream));
 }
 
 int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const int64_t *word_off,
@@ -1115,7 +1129,7 @@ int sc_decompress_chunks_static(const sc_model *m, const uint32_t *words, const 
     int32_t *stat_dev = (int32_t *)((char *)base + SCRATCH_STATE_BYTES);
     uint8_t *xch = (uint8_t *)base + SCRATCH_STATE_BYTES + 256;
     return decompress_run(m, words, word_off, word_cnt, lengths, n_chunks, tokens, tok_off, status, lengths_host,
-                          state, stat_dev, xch, XCH_MAX_GROUPS, as_stream(stream));
+                          state, stat_dev, xch, XCH_MAX_GROUPS, 0, as_stream(stream));
 }
 
 }  // extern "C"

@@ -54,9 +54,14 @@ def _h2d(a, dev):
     (stream-ordered on the current stream; torch keeps the pinned block
     until the copy is done)."""
     a = np.ascontiguousarray(a)
-    pin = torch.empty(a.shape, dtype=torch.from_numpy(a[:0]).dtype, pin_memory=True)
+    pin = torch.empty(a.shape, dtype=_TORCH_DTYPE[a.dtype], pin_memory=True)
     pin.numpy()[...] = a
     return pin.to(dev, non_blocking=True)
+
+
+_TORCH_DTYPE = {np.dtype(k): v for k, v in ((np.uint8, torch.uint8), (np.int8, torch.int8), (np.int16, torch.int16),
+                                              (np.int32, torch.int32), (np.int64, torch.int64),
+                                              (np.uint16, torch.uint16), (np.uint32, torch.uint32))}
 
 
 def _to_device(a, dev):
@@ -443,7 +448,15 @@ class QuantMLPCompression(ReadFramingMixin):
             h_tokens.copy_(tokens, non_blocking=True)
             h_status.copy_(status, non_blocking=True)
             torch.cuda.current_stream().synchronize()
-        st = h_status.numpy()
+            st = h_status.numpy()
+            late = np.flatnonzero(st == _hip.SC_STATUS_SYNC_TIMEOUT)
+            if len(late):
+                # a split launch whose workgroups timed out waiting for each
+                # other (one of them was not scheduled in time): its chunks
+                # are decoded again, each an independent stream, by unsplit
+                # launches that never wait between workgroups
+                self._redecode_unsplit(late, word_off[order], cnt[order], len_host, tok_off[order], t_words,
+                                       tokens, h_tokens, st)
         if st.any():
             bad = np.flatnonzero(st)
             if (st[bad] == _hip.SC_STATUS_SYNC_TIMEOUT).any():
@@ -451,3 +464,24 @@ class QuantMLPCompression(ReadFramingMixin):
             raise ValueError("invalid range stream or mismatching entropy model in chunk "
                              f"{int(order[bad[0]])}")
         return h_tokens.numpy()[:n_tokens], tok_off
+
+    def _redecode_unsplit(self, rows, woff, cnt, lens, toff, t_words, tokens, h_tokens, st):
+        """Decode the chunks `rows` (indices into the sorted arrays) again with
+        SC_DEC_OPT_NO_SPLIT into the same device token buffer, refresh the
+        host copy and their entries of `st` (the host status array)."""
+        dev = self.hip.device
+        m = len(rows)
+        sub_len = np.ascontiguousarray(lens[rows], np.int32)
+        d = lambda a: _h2d(np.ascontiguousarray(a), dev)
+        t_woff, t_cnt, t_len, t_toff = d(woff[rows]), d(cnt[rows]), d(sub_len), d(toff[rows])
+        status = torch.empty(m, dtype=torch.int32, device=dev)
+        ws = self._decompress_workspace(m)
+        _hip.check(_hip.lib().sc_decompress_chunks_opts(
+            self.hip.handle, _hip.ptr(t_words), _hip.ptr(t_woff), _hip.ptr(t_cnt), _hip.ptr(t_len), m,
+            _hip.ptr(tokens), _hip.ptr(t_toff), _hip.ptr(status), sub_len.ctypes.data, _hip.ptr(ws), ws.numel(),
+            _hip.SC_DEC_OPT_NO_SPLIT, _hip.stream_ptr()))
+        h_tokens.copy_(tokens, non_blocking=True)
+        h_sub = torch.empty(m, dtype=torch.int32, pin_memory=True)
+        h_sub.copy_(status, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        st[rows] = h_sub.numpy()

@@ -66,6 +66,8 @@ def decode_many(blobs, counts, fallback_bits: int = 32, max_quotient: int = MAX_
     counts = np.ascontiguousarray(counts, np.int64)
     if len(counts) != n:
         raise ValueError("one count per blob")
+    if n and int(counts.min()) < 0:
+        raise ValueError("Rice value counts must be non-negative")
     kept = [np.frombuffer(bytes(b), np.uint8) if len(b) else np.zeros(1, np.uint8) for b in blobs]
     ptrs = np.fromiter((a.ctypes.data for a in kept), np.uint64, count=n)
     lens = np.fromiter((len(b) for b in blobs), np.int64, count=n)

@@ -70,6 +70,66 @@ def test_mlp_context_several_tiles_per_workgroup(gpu, oracle_mod, mode):
     assert checked == 9   # workgroup 0 runs three tiles (its third one partial), the others two
 
 
+def test_c2_full_launch_against_oracle(gpu, oracle_mod):
+    """The c2 launch at its full size: 1,048,576 context rows of the c2 model
+    (per-channel constants, the bench's rows) -> int32 CDF tables in one
+    launch, one workgroup per CU, so workgroup b runs the 32 tiles b, b +
+    n_cu, ..., b + 31 n_cu.  Its first, middle and last tiles (b, b + 16
+    n_cu, b + 31 n_cu) of four workgroups against the oracle."""
+    from sigcomp_amd import signal, synth
+    from sigcomp_amd.model_io import random_int_model
+    from sigcomp_amd.quant_mlp_export import HipModel
+    n_cu = _n_cu()
+    rows = 1 << 20
+    m = random_int_model(seed=2, per_channel=True)
+    hm = HipModel(m, gpu)
+    toks = np.concatenate([signal.split_signal(r)[1] for r in synth.synth_reads(64, 202, synth.DNA)])
+    toks = toks.astype(np.int64)
+    starts = np.random.default_rng(3).integers(-63, len(toks) - 64, rows)
+    idx = starts[:, None] + np.arange(64)[None, :]
+    ctx = np.where(idx < 0, 256, toks[np.clip(idx, 0, None)])
+    out = hm.forward_windows(torch.from_numpy(ctx).to(gpu), "cdf")
+    n_tiles = rows // 128
+    om = oracle_mod.OracleModel(m)
+    tiles = sorted({b + k * n_cu for b in (0, 1, n_cu // 2, n_cu - 1) for k in (0, 16, 31) if b + k * n_cu < n_tiles})
+    assert len(tiles) == 12
+    for tile in tiles:
+        sl = slice(tile * 128, tile * 128 + 128)
+        ref = oracle_mod.logits_to_cdf(oracle_mod.mlp_forward(om, ctx[sl]), m.exp_lut)
+        assert np.array_equal(out[sl].cpu().numpy().astype(np.int64), ref.astype(np.int64)), tile
+
+
+def test_c1_full_config_split_decode_every_chunk_against_oracle(gpu, oracle_mod, capfd, monkeypatch):
+    """Config c1 (BASELINE.json's CPU case, 64 reads, 675 chunks) through the
+    HIP path: compress_flat, then decompress_flat, whose single launch of
+    22 groups of 32 chunks runs split (8 workgroups per group sharing layer
+    0, one exchange per step) over eight 256-step segments.  Every chunk's
+    bytes equal the oracle's and every decoded chunk equals its input."""
+    from sigcomp_amd import model_io, signal, synth
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    cfg = synth.CONFIGS["c1"]
+    codec = QuantMLPCompression(chunk_len=2048, gpu=0, model_path=model_io.DEFAULT_QUANT_LOSSLESS_MODEL_PATH)
+    small = signal.reads_tokens(signal.split_reads(synth.config_reads("c1"), cfg["lsb"]))
+    chunks = [s[i:i + 2048] for s in small for i in range(0, len(s), 2048)]
+    lengths = np.array([len(c) for c in chunks], np.int32)
+    tokens = np.concatenate(chunks)
+    print(f"[c1] {len(chunks)} chunks, {len(tokens)} tokens", flush=True)
+    assert len(chunks) < 32 * _n_cu()
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    capfd.readouterr()
+    monkeypatch.setenv("SC_HIP_DEC_LOG", "1")
+    monkeypatch.delenv("SC_HIP_DEC_SEG", raising=False)
+    monkeypatch.delenv("SC_HIP_DEC_SPLIT", raising=False)
+    back, tok_off = codec.decompress_flat(words, woff, wcnt, lengths)
+    log = capfd.readouterr().err
+    assert "split launch p8" in log and "seg 256" in log, log
+    assert int(lengths.max()) == 2048
+    assert np.array_equal(back, tokens)
+    ref = oracle_mod.compress_chunks(oracle_mod.OracleModel(codec.model), chunks)
+    for i in range(len(chunks)):
+        assert words[woff[i]:woff[i] + wcnt[i]].tobytes() == ref[i], i
+
+
 def _oracle_pick(lengths, n_cu, rng):
     """Chunk indices (in the caller's order) to check against the oracle:
     with chunks sorted longest first (as decompress_flat sorts them), the 16

@@ -123,3 +123,29 @@ def test_generic_model_loaded_by_dims(tmp_path, oracle_mod):
     assert codec.hip.core == 3 and codec.window_size == 12
     chunk = np.random.default_rng(1).integers(0, 30, 700).astype(np.uint8)
     assert codec.compress_chunks([chunk]) == oracle_mod.compress_chunks(oracle_mod.OracleModel(m), [chunk])
+
+
+def test_generic_wide_model_batches_within_its_scratch_bound(oracle_mod):
+    """A model 524,288 inputs wide (window 512 x 1,024-wide embedding): the
+    generic path's scratch per call is bounded (1 GiB), so its batches
+    shrink to 960 rows (forward, decode) and 7 tiles of 128 steps
+    (compress) instead of 65,536 rows, which would need 64 GiB.  Forward on
+    2,100 rows (three batches) and compress / decompress of chunks spanning
+    two compress batches, bit-exact against the oracle."""
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from sigcomp_amd.model_io import random_int_model
+    from sigcomp_amd.quant_mlp_export import QuantMLPCompression
+    m = random_int_model(seed=21, window=512, emb_dim=1024, hidden=64, n_hidden=1, per_channel=True)
+    codec = QuantMLPCompression(chunk_len=1000, gpu=0, model=m)
+    assert codec.hip.core == 3
+    om = oracle_mod.OracleModel(m)
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(0, 257, (2100, m.window)).astype(np.int64)
+    got = codec.hip.forward_windows(torch.from_numpy(ctx).cuda(), "logits").cpu().numpy()
+    assert np.array_equal(got, oracle_mod.mlp_forward(om, ctx))
+    chunks = [rng.integers(0, 40, n).astype(np.uint8) for n in (130, 7, 1000)]
+    comp = codec.compress_chunks(chunks)
+    assert comp == oracle_mod.compress_chunks(om, chunks)
+    back = codec.decompress_chunks(comp, [len(c) for c in chunks])
+    assert all(np.array_equal(a, b) for a, b in zip(chunks, back))

@@ -776,20 +776,28 @@ def test_split_decode_corrupt_chunks(codecs, monkeypatch):
             assert np.array_equal(back[s], tokens[s]), i
 
 
-def test_split_decode_timeout_reports_status(codecs, monkeypatch):
+def test_split_decode_timeout_reports_status_and_redecodes_unsplit(codecs, monkeypatch):
     """With a spin limit of 0 polls (SC_HIP_DEC_SPIN=0; the default is
     2**18) every wait of a split decode gives up at once: every chunk of
-    every group reports SC_STATUS_SYNC_TIMEOUT, also through later step
-    segments, and decompress_flat raises RuntimeError.  The kernels end
-    normally, and the next decode is correct."""
+    every group reports SC_STATUS_SYNC_TIMEOUT through the C ABI, also
+    through later step segments, and the kernels end normally.
+    decompress_flat then decodes the timed-out chunks again with unsplit
+    launches (SC_DEC_OPT_NO_SPLIT), which never wait, and returns the input;
+    the next decode with the default limit is correct as well.  A corrupt
+    chunk among them is still reported as such."""
     codec = codecs["lossless"]
     tokens, lengths, words, woff, wcnt = _random_chunks(codec, 40, 300, 9)
     monkeypatch.setenv("SC_HIP_DEC_SPIN", "0")
     monkeypatch.setenv("SC_HIP_DEC_SEG", "64")
     _, status, _ = _decode_direct(codec, words, woff, wcnt, lengths)
     assert (status == 4).all(), status   # SC_STATUS_SYNC_TIMEOUT
-    with pytest.raises(RuntimeError, match="timed out"):
-        codec.decompress_flat(words, woff, wcnt, lengths)
+    back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
+    assert np.array_equal(back, tokens)
+    bad = words.copy()
+    c = int(np.argmax(lengths))
+    bad[woff[c]:woff[c] + wcnt[c]] = 0xFFFFFFFF
+    with pytest.raises(ValueError, match="invalid range stream"):
+        codec.decompress_flat(bad, woff, wcnt, lengths)
     monkeypatch.delenv("SC_HIP_DEC_SPIN")
     back, _ = codec.decompress_flat(words, woff, wcnt, lengths)
     assert np.array_equal(back, tokens)

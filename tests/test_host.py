@@ -98,6 +98,80 @@ def test_reassemble_inverts_split(lsb):
         assert np.array_equal(b, ref.lossy_decode(rr, lsb) if lsb else rr)
 
 
+def _wrap16(x):
+    """Two's-complement int16 value of the integer x (x mod 2**16, signed)."""
+    return ((x + 32768) % 65536) - 32768
+
+
+def _lossy_closed_forms(b):
+    """The lossy LSB transform of main.py:158-171 stated arithmetically, in
+    int64 floor division rather than the reference's masks and shifts:
+    reduce = round half up to a multiple of 2**b (floor((v + 2**(b-1)) / 2**b)
+    * 2**b), wrapped to int16; encode = floor(x / 2**b); decode = x * 2**b
+    wrapped to int16.  -> (v, reduce(v), encode(reduce(v)), decode(encode(...)))
+    over every int16 value v."""
+    v = np.arange(-32768, 32768, dtype=np.int64)
+    step = 2 ** b
+    red = _wrap16((v + step // 2) // step * step)
+    enc = red // step
+    dec = _wrap16(enc * step)
+    return v, red, enc, dec
+
+
+@pytest.mark.parametrize("lsb", list(range(1, 16)))
+def test_lossy_transform_closed_form_every_int16(lsb):
+    """Pins the oracle's lossy restatement (signal_ref.reduce_lsb /
+    lossy_encode / lossy_decode) and the C++ split / reassembly against the
+    closed form over all 65,536 int16 samples for lsb 1..15, incl. ties
+    (v = k * 2**b + 2**(b-1) rounds up, also below zero) and the wrap of
+    32767 rounded up past the int16 range."""
+    import signal_ref as ref
+    v, red, enc, dec = _lossy_closed_forms(lsb)
+    v16 = v.astype(np.int16)
+    assert np.array_equal(ref.reduce_lsb(v16, lsb).astype(np.int64), red)
+    assert np.array_equal(ref.lossy_encode(red.astype(np.int16), lsb).astype(np.int64), enc)
+    assert np.array_equal(ref.lossy_decode(enc.astype(np.int16), lsb).astype(np.int64), dec)
+    assert np.array_equal(ref.prepare_signal(v16, lsb).astype(np.int64), enc)
+    # special cases in plain Python integers
+    half = 1 << (lsb - 1)
+    assert int(ref.reduce_lsb(np.array([half], np.int16), lsb)[0]) == _wrap16(1 << lsb)   # tie rounds up
+    assert int(ref.reduce_lsb(np.array([-half], np.int16), lsb)[0]) == 0                  # -1/2 rounds up to 0
+    assert int(ref.reduce_lsb(np.array([half - 1], np.int16), lsb)[0]) == 0
+    top = _wrap16(((32767 + half) >> lsb) << lsb)            # 32767 rounds to 2**15: wraps to -32768
+    assert int(ref.reduce_lsb(np.array([32767], np.int16), lsb)[0]) == top == -32768
+    assert int(ref.reduce_lsb(np.array([-32768], np.int16), lsb)[0]) == -32768
+    # the C++ host library: one read of every int16 value (in order, then
+    # shuffled, so the deltas vary), split with lsb and reassembled
+    _lib_or_skip()
+    from sigcomp_amd import signal
+    perm = np.random.default_rng(lsb).permutation(65536)
+    reads = [v16, v16[perm]]
+    sp = signal.split_reads(reads, lsb)
+    for i, (r, e) in enumerate(zip(reads, [enc, enc[perm]])):
+        s0, sm, la, lg = ref.split_signal(e.astype(np.int16))
+        o, n = sp["small_off"][i], sp["n_small"][i]
+        assert int(sp["sig0"][i]) == s0 == int(e[0])
+        assert np.array_equal(sp["small"][o:o + n], sm)
+        lo, ln = sp["large_off"][i], sp["n_large"][i]
+        assert np.array_equal(sp["large_adj"][lo:lo + ln], la)
+        assert np.array_equal(sp["large_gap"][lo:lo + ln], lg)
+    back = signal.reassemble_reads(sp, lsb=lsb)
+    assert np.array_equal(back[0].astype(np.int64), dec)
+    assert np.array_equal(back[1].astype(np.int64), dec[perm])
+
+
+def test_lossy_closed_form_rejects_plausible_misreadings():
+    """The closed form is not a restatement of itself: a round-half-down
+    reading, a missing int16 wrap or a logical shift would each differ."""
+    v, red, enc, dec = _lossy_closed_forms(3)
+    half_down = _wrap16((v + 3) // 8 * 8)
+    assert not np.array_equal(half_down, red)
+    no_wrap = (v + 4) // 8 * 8
+    assert not np.array_equal(no_wrap, red)
+    logical = (red & 0xFFFF) >> 3
+    assert not np.array_equal(logical, enc)
+
+
 def test_reassemble_and_split_errors():
     _lib_or_skip()
     from sigcomp_amd import signal

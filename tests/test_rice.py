@@ -107,7 +107,7 @@ def test_split_side_streams_round_trip():
     assert all(np.array_equal(a, b) for a, b in zip(reads, out))
 
 
-@pytest.mark.parametrize("case", ["truncated", "trailing", "padding", "k", "short", "quotient"])
+@pytest.mark.parametrize("case", ["truncated", "trailing", "padding", "k", "short", "quotient", "fallback"])
 def test_malformed_blobs_rejected(case):
     v = np.array([9, 2, 7, 300, 1], np.uint32)
     b = bytearray(rice.rice_encode(v, 16))
@@ -124,12 +124,38 @@ def test_malformed_blobs_rejected(case):
         b[0] = 17
     elif case == "short":
         b = b[:1]
+    elif case == "fallback":
+        # k = 16, q = 1, low bits 5: the value 65541 does not fit 16 bits
+        b = bytearray([16, 0x15, 0x00, 0x00])
+        n = 1
     else:
         # k = 31 and a quotient of 2: no 32-bit value has it
         b = bytearray([31, 0b011])
         n = 1
     with pytest.raises(ValueError, match="Rice"):
         rice.rice_decode(bytes(b), n, 16 if case != "quotient" else 32)
+
+
+def test_negative_count_rejected_before_anything_is_written():
+    """A negative count beside a valid item: the Python boundary raises, and
+    the C ABI returns SC_ERR_ARG naming the item without writing any value
+    (the output offsets after a negative count would not be valid)."""
+    import ctypes
+    from sigcomp_amd import _host
+    blob = rice.rice_encode(np.array([1, 2, 3], np.uint32), 32)
+    with pytest.raises(ValueError, match="non-negative"):
+        rice.decode_many([b"\x00", blob], [-3, 3], 32)
+    kept = [np.zeros(1, np.uint8), np.frombuffer(blob, np.uint8)]
+    ptrs = np.array([a.ctypes.data for a in kept], np.uint64)
+    lens = np.array([1, len(blob)], np.int64)
+    counts = np.array([-3, 3], np.int64)
+    out_off = np.array([0, 0], np.int64)
+    out = np.full(8, 0xDEADBEEF, np.uint32)
+    bad = ctypes.c_int64(-1)
+    rc = _host.lib().sc_rice_decode(_host._p(ptrs), _host._p(lens), _host._p(counts), 2, 32, 31, _host._p(out),
+                                    _host._p(out_off), 1, ctypes.byref(bad))
+    assert rc != 0 and bad.value == 0
+    assert (out == 0xDEADBEEF).all()
 
 
 def test_value_outside_fallback_width_rejected():

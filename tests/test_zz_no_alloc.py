@@ -130,3 +130,46 @@ def test_static_entry_under_graph_capture(codec):
         torch.cuda.synchronize()
         assert np.array_equal(status.cpu().numpy(), ref_st), rep
         assert np.array_equal(out.cpu().numpy(), ref_tok), rep
+
+
+def test_device_lengths_refused_under_graph_capture(codec):
+    """Without the host copy of the lengths the launch plan would read them
+    back from the device, a wait that a capturing stream cannot hold: both
+    decode entries return SC_ERR_ARG before enqueuing anything, so the
+    caller's capture stays valid; a call with host lengths captured after
+    the refused ones replays correctly."""
+    from sigcomp_amd import _hip
+    L = _hip.lib()
+    tokens, lengths, words, woff, wcnt = _inputs(codec, 40, 100, 300, 7)
+    n = len(lengths)
+    ref_tok, ref_st = _decode(codec, "static", words, woff, wcnt, lengths, True)
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(lengths[:-1], dtype=np.int64, out=tok_off[1:])
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_words, t_woff, t_cnt = d(words.view(np.int32)), d(woff.astype(np.int64)), d(wcnt.astype(np.int32))
+    t_len, t_toff = d(lengths.astype(np.int32)), d(tok_off)
+    out = torch.empty(int(lengths.sum()), dtype=torch.uint8, device="cuda")
+    status = torch.empty(n, dtype=torch.int32, device="cuda")
+    ws = codec._decompress_workspace(n)
+    len_host = np.ascontiguousarray(lengths, np.int32)
+    torch.cuda.synchronize()
+    args = lambda hl: [codec.hip.handle, t_words.data_ptr(), t_woff.data_ptr(), t_cnt.data_ptr(), t_len.data_ptr(),
+                       n, out.data_ptr(), t_toff.data_ptr(), status.data_ptr(), hl]
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        s = torch.cuda.current_stream().cuda_stream
+        rc_static = L.sc_decompress_chunks_static(*args(None), s)
+        err_static = L.sc_last_error()
+        rc_ws = L.sc_decompress_chunks(*args(None), ws.data_ptr(), ws.numel(), s)
+        _hip.check(L.sc_decompress_chunks_static(*args(len_host.ctypes.data), s))
+    assert rc_static == _hip.SC_ERR_ARG and rc_ws == _hip.SC_ERR_ARG
+    assert b"graph capture" in err_static
+    for rep in range(2):
+        out.fill_(0xAB)
+        status.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(status.cpu().numpy(), ref_st), rep
+        assert np.array_equal(out.cpu().numpy(), ref_tok), rep
