@@ -83,10 +83,12 @@ class PowerSampler:
     power); window(t0, t1) averages the samples of a time.monotonic()
     interval.  Inactive (None results) where the sysfs file is absent."""
 
-    def __init__(self, period=0.02):
-        files = sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_input") +
-                       glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_average"))
+    def __init__(self, period=0.02, files=None, scale=1e-6):
+        if files is None:
+            files = sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_input") +
+                           glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_average"))
         self.path = files[0] if files else None
+        self.scale = scale
         self.samples = []
         self.proc = None
         if self.path:
@@ -98,7 +100,7 @@ class PowerSampler:
     def _read(self):
         for line in self.proc.stdout:
             t, p = line.split()
-            self.samples.append((float(t), int(p) * 1e-6))
+            self.samples.append((float(t), int(p) * self.scale))
 
     def window(self, t0, t1):
         if not self.proc:
@@ -179,7 +181,7 @@ def roofline(kernel, tokens, seconds, config, direction):
             "traffic": pmc_traffic(config, kernel),
             "traffic_source": f"profiles/traffic_{config}.txt (rocprofv3 PMC, bytes per call)",
             "algorithmic": f"{OPS_PER_ROW} int8 ops per {direction} token x {tokens} tokens per call",
-            **ceiling_fields(achieved), **pmc_mfma(config, kernel)}
+            **ceiling_fields(achieved, config), **pmc_mfma(config, kernel)}
 
 
 PEAK_L1_GBS_PER_CU = 64 * 2.4   # vector L1 fill: 64 bytes per clock at the 2.4 GHz peak engine clock
@@ -578,7 +580,7 @@ def run_mlp(rows, steps, warmup, sampler, copy_mib=0):
                          "traffic": pmc_traffic("c2", "k_mlp_context"),
                          "traffic_source": "profiles/traffic_c2.txt (rocprofv3 PMC, bytes per launch)",
                          "algorithmic": f"{OPS_PER_ROW} int8 ops per row x {rows} rows per launch",
-                         **ceiling_fields(achieved), **pmc_mfma("c2", "k_mlp_context")},
+                         **ceiling_fields(achieved, "c2"), **pmc_mfma("c2", "k_mlp_context")},
             "same_rows_other_models": {**side, "note": "the same rows and kernel with a random per-tensor model "
                                                        "and with the bundled lossless checkpoint; not the c2 figure"}}
 
@@ -594,49 +596,134 @@ def bench_mlp(args):
 
 # ------------------------------------------------------- ceiling, coder
 
+# Share of a token's int8 MACs in layer 0 (8192 -> 512); the rest are the
+# hidden and output layers (512-wide inputs).
+LAYER0_MAC_SHARE = 8192 * 512 / (OPS_PER_ROW // 2)
+
+
+def _a_frag(m):
+    """32 x 32 int8 block M[m][k] -> one A fragment of v_mfma_i32_32x32x32_i8
+    (lane l holds M[l % 32][16 (l // 32) .. +15])."""
+    return np.ascontiguousarray(m.reshape(32, 2, 16).transpose(1, 0, 2).reshape(64, 16))
+
+
+def _b_frag(m):
+    """32 x 32 int8 block M[k][n] -> one B fragment (lane l holds
+    M[16 (l // 32) .. +15][l % 32])."""
+    return np.ascontiguousarray(m.reshape(2, 16, 32).transpose(0, 2, 1).reshape(64, 16))
+
+
+def _requant(acc, layer):
+    """(acc + bias) * M0 >> shift, clamped to int8 (ReLU layers at 0): the
+    integer linear layer's epilogue, in int64."""
+    y = (acc + layer.bias.astype(np.int64)) * layer.m0.astype(np.int64) >> layer.shift.astype(np.int64)
+    return np.clip(y, 0 if layer.relu else -128, 127).astype(np.int8)
+
+
+def checkpoint_operands(model, cfg_name, seed=7):
+    """MFMA operand sets of a bundled checkpoint as the codec feeds them:
+    {"layer0": 4 A fragments of layer-0 weights and 4 B fragments of 32
+    embedded context rows (tokens of the config's synthetic reads),
+    "hidden": 4 A fragments of hidden-layer weights and 4 B fragments of the
+    same rows' layer-0 outputs (ReLU activations)} as 8192-byte arrays."""
+    from sigcomp_amd import signal, synth
+    cfg = synth.CONFIGS[cfg_name]
+    rng = np.random.default_rng(seed)
+    toks = np.concatenate([signal.split_signal(r, cfg["lsb"])[1]
+                           for r in synth.synth_reads(8, cfg["seed"], cfg["profile"])]).astype(np.int64)
+    starts = rng.integers(0, len(toks) - 64, 32)
+    ctx = toks[starts[:, None] + np.arange(64)[None, :]]
+    x0 = model.emb[ctx].reshape(32, 64 * model.emb.shape[1]).astype(np.int64)   # [rows, 8192]
+    L0 = model.layers[0]
+    x1 = _requant((x0.astype(np.float64) @ L0.weight.astype(np.float64).T).astype(np.int64), L0)  # exact
+    sets = {}
+    for name, w_layers, act in (("layer0", [L0], x0), ("hidden", model.layers[1:-1], x1.astype(np.int64))):
+        frags_a, frags_b = [], []
+        for j in range(4):
+            W = w_layers[j % len(w_layers)].weight
+            nt, kt = rng.integers(0, W.shape[0] // 32), rng.integers(0, W.shape[1] // 32)
+            frags_a.append(_a_frag(W[nt * 32:nt * 32 + 32, kt * 32:kt * 32 + 32]))
+            kb = rng.integers(0, act.shape[1] // 32)
+            frags_b.append(_b_frag(act[:, kb * 32:kb * 32 + 32].T.astype(np.int8)))
+        sets[name] = np.concatenate(frags_a + frags_b).reshape(-1).astype(np.int8)
+    return sets
+
+
 def bench_ceiling(args):
-    """The int8 MFMA rate the GPU sustains at its power limit: every CU runs
-    register-operand v_mfma_i32_32x32x32_i8 chains (sc_mfma_burn_i8) for
-    about 6 s per operand set (long enough for the power controller to settle)
-    with random int8 operands (the data the codec's MFMAs see) and with
-    zeros (no toggling: close to the clock-limited 5.0 POP/s)."""
+    """The int8 MFMA rate the GPU sustains at its power limit, per operand
+    data: every CU runs register-operand v_mfma_i32_32x32x32_i8 chains
+    (sc_mfma_burn_i8) for about 6 s per operand set (long enough for the
+    power controller to settle), with uniform random int8 operands, with
+    zeros (no toggling: close to the clock-limited 5.0 POP/s), and with the
+    operands the codec's MFMAs see for each bundled checkpoint: layer-0
+    weight fragments against embedded context rows of the config's
+    synthetic reads, and hidden-layer weight fragments against those rows'
+    ReLU activations.  A checkpoint's ceiling weights the two by their share
+    of a token's MACs (layer 0: 68.1%).  Socket power and, where hwmon has
+    it, the GFX clock are sampled over each set."""
     import torch
     from sigcomp_amd import _hip
+    from sigcomp_amd.model_io import (DEFAULT_QUANT_LOSSLESS_MODEL_PATH, DEFAULT_QUANT_LOSSY_MODEL_PATH,
+                                      load_int_model)
     L = _hip.lib()
     n_groups = torch.cuda.get_device_properties(0).multi_processor_count
     iters = 5000
     ops_per_launch = n_groups * 4 * iters * 64 * 65536
     out = torch.empty(n_groups * 256 * 16, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
-    res = {}
     g = torch.Generator().manual_seed(1)
-    for name in ("random", "zero"):
-        ops = (torch.randint(-128, 128, (8192,), dtype=torch.int8, generator=g) if name == "random"
-               else torch.zeros(8192, dtype=torch.int8)).cuda()
-        rc = L.sc_mfma_burn_i8(ops.data_ptr(), 10, n_groups, out.data_ptr(), stream)
-        if rc:
-            raise RuntimeError(L.sc_last_error().decode())
-        torch.cuda.synchronize()
-        rates = []
-        t_end = time.time() + 6.0
-        while time.time() < t_end:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            L.sc_mfma_burn_i8(ops.data_ptr(), iters, n_groups, out.data_ptr(), stream)
-            e1.record()
+    sets = {"random": torch.randint(-128, 128, (8192,), dtype=torch.int8, generator=g).numpy(),
+            "zero": np.zeros(8192, np.int8)}
+    for tag, path, cfg in (("lossless", DEFAULT_QUANT_LOSSLESS_MODEL_PATH, "c3"),
+                           ("lossy", DEFAULT_QUANT_LOSSY_MODEL_PATH, "c5")):
+        for k, v in checkpoint_operands(load_int_model(path), cfg).items():
+            sets[f"{tag}_{k}"] = v
+    power = PowerSampler()
+    clk_files = sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/freq1_input"))
+    clock = PowerSampler(period=0.05, files=clk_files, scale=1e-6) if clk_files else None   # Hz -> MHz
+    res = {}
+    try:
+        for name, arr in sets.items():
+            ops = torch.from_numpy(arr.copy()).cuda()
+            rc = L.sc_mfma_burn_i8(ops.data_ptr(), 10, n_groups, out.data_ptr(), stream)
+            if rc:
+                raise RuntimeError(L.sc_last_error().decode())
             torch.cuda.synchronize()
-            rates.append(ops_per_launch / (e0.elapsed_time(e1) / 1e3) / 1e12)
-        # the last second: the steady state under the power limit
-        tail = rates[-max(1, len(rates) // 6):]
-        res[name] = round(float(np.median(tail)), 1)
-        log(f"[bench] MFMA burn, {name} operands: {res[name]} TOP/s (median of the last {len(tail)} launches)")
-    return {"metric": "sustained int8 MFMA rate (register operands, all CUs)", "value": res["random"],
-            "unit": "TOP/s", "n_gpus": 1, "steps": len(rates), "warmup": 1, "ms_per_step": None,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-            "data": "synthetic", "config": {"workload": f"{n_groups} workgroups x 4 waves x {iters * 64} "
-                                                        "v_mfma_i32_32x32x32_i8 per launch"},
-            "zero_operands_tops": res["zero"], "peak": PEAK_INT8_TOPS,
-            "frac_of_peak": round(res["random"] / PEAK_INT8_TOPS, 4)}
+            rates = []
+            t_end = time.time() + 6.0
+            while time.time() < t_end:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                L.sc_mfma_burn_i8(ops.data_ptr(), iters, n_groups, out.data_ptr(), stream)
+                e1.record()
+                torch.cuda.synchronize()
+                rates.append((time.monotonic(), ops_per_launch / (e0.elapsed_time(e1) / 1e3) / 1e12))
+            # the last second: the steady state under the power limit
+            tail = rates[-max(1, len(rates) // 6):]
+            t0 = tail[0][0] - (tail[1][0] - tail[0][0] if len(tail) > 1 else 0.2)
+            pw = power.window(t0, tail[-1][0])
+            ck = clock.window(t0, tail[-1][0]) if clock else None
+            res[name] = {"tops": round(float(np.median([r for _, r in tail])), 1),
+                         "socket_w": pw["avg_w"] if pw else None, "gfx_mhz": ck["avg_w"] if ck else None,
+                         "mean_abs_operand": round(float(np.abs(arr.astype(np.int32)).mean()), 2)}
+            log(f"[bench] MFMA burn, {name} operands: {res[name]}")
+    finally:
+        power.stop()
+        if clock:
+            clock.stop()
+    for tag in ("lossless", "lossy"):
+        r0, rh = res[f"{tag}_layer0"]["tops"], res[f"{tag}_hidden"]["tops"]
+        res[f"{tag}_checkpoint"] = {"tops": round(1.0 / (LAYER0_MAC_SHARE / r0 + (1 - LAYER0_MAC_SHARE) / rh), 1),
+                                    "note": "layer-0 and hidden-layer operand rates weighted by their share of "
+                                            "a token's MACs (time-weighted harmonic mean)"}
+    return {"metric": "sustained int8 MFMA rate (register operands, all CUs)",
+            "value": res["lossless_checkpoint"]["tops"], "unit": "TOP/s", "n_gpus": 1, "steps": 1, "warmup": 1,
+            "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8", "data": "synthetic operands and the bundled checkpoints' own",
+            "config": {"workload": f"{n_groups} workgroups x 4 waves x {iters * 64} v_mfma_i32_32x32x32_i8 per "
+                                   "launch, ~6 s per operand set"},
+            "operand_sets": res, "peak": PEAK_INT8_TOPS,
+            "frac_of_peak": {k: round(v["tops"] / PEAK_INT8_TOPS, 4) for k, v in res.items()}}
 
 
 # Algorithmic HBM bytes per stream and step of the coder step kernels
@@ -668,6 +755,7 @@ def bench_coder(args):
     L = _hip.lib()
     stream = torch.cuda.current_stream(dev).cuda_stream
     lut = torch.from_numpy(load_int_model().exp_lut.astype(np.int64)).to(dev)
+    calibration_copy(dev, args.copy_mib)
     T = max(2, args.steps)
     out = {}
     for B in (args.rows, 20480):
@@ -737,23 +825,32 @@ def bench_coder(args):
             "kernels": {str(B): v for B, v in out.items()}}
 
 
-def power_capped_peak():
-    """Sustained int8 MFMA rate with random operands, measured by
+# Operand data each configuration's MFMAs see -> the ceiling it is read
+# against: the bundled checkpoints' own (c1, c3/c4 lossless; c5 lossy) and
+# uniform random for c2's random model.
+CEILING_OPERANDS = {"c1": "lossless_checkpoint", "c3": "lossless_checkpoint", "c4": "lossless_checkpoint",
+                    "c5": "lossy_checkpoint", "c2": "random_operands"}
+
+
+def power_capped_peak(operands="lossless_checkpoint"):
+    """Sustained int8 MFMA rate for the given operand data, measured by
     `bench.py --config ceiling` and recorded in profiles/mfma_ceiling.txt."""
     f = REPO / "profiles" / "mfma_ceiling.txt"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
-        if line.startswith("random_operands_tops"):
+        if line.startswith(operands + "_tops"):
             return float(line.split()[1])
     return None
 
 
-def ceiling_fields(achieved):
-    cap = power_capped_peak()
+def ceiling_fields(achieved, config):
+    operands = CEILING_OPERANDS.get(config, "lossless_checkpoint")
+    cap = power_capped_peak(operands)
     if cap is None:
         return {}
     return {"power_capped_peak": cap, "frac_of_power_capped_peak": round(achieved / cap, 4),
+            "power_capped_peak_operands": operands,
             "power_capped_peak_source": "profiles/mfma_ceiling.txt (bench.py --config ceiling)"}
 
 
