@@ -209,15 +209,41 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
     mlp_tile_init<CORE>(M, s_par, wave, lane);
     static_assert(R_TILE + WIN <= THREADS, "one staged token per thread");
     const int32_t n_tiles = (int32_t)min<int64_t>(tile_start[n_chunks], max_desc);
-    // The next tile's descriptor is loaded during this tile's epilogue.
-    int4 d = (int32_t)blockIdx.x < n_tiles ? desc[blockIdx.x] : make_int4(0, 0, 0, 0);
-    for (int32_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        const int64_t base = (int64_t)(uint32_t)d.x | ((int64_t)d.y << 32);   // token t0 of the chunk
-        const int32_t rem = d.z, t0 = d.w;                                     // L - t0, t0
-        // s_tok[i] <-> sequence position t0 - 64 + i (SOS before 0)
+    const int32_t G = (int32_t)gridDim.x;
+    // This thread's staged token of the tile with descriptor dd: s_tok[i]
+    // <-> sequence position t0 - 64 + i (SOS before 0).
+    auto stage_token = [&](const int4 &dd) {
+        const int64_t b = (int64_t)(uint32_t)dd.x | ((int64_t)dd.y << 32);
         const int32_t p = (int32_t)threadIdx.x - WIN;
         int v = 0;
-        if (threadIdx.x < R_TILE + WIN) v = t0 + p < 0 ? SOS : (p < rem ? (int)tokens[base + p] : 0);
+        if (threadIdx.x < R_TILE + WIN) v = dd.w + p < 0 ? SOS : (p < dd.z ? (int)tokens[b + p] : 0);
+        return v;
+    };
+    // a buffer (vector memory) load: a scalar one, which a load of a
+    // uniform address would become, would be waited for with the epilogue's
+    // first LDS reads, since they share its counter
+    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)desc, (short)0, (int)min<int64_t>((int64_t)n_tiles * 16, INT32_MAX), 0x00020000);
+    auto desc_at = [&](int32_t k) {
+        if (k >= n_tiles) return make_int4(0, 0, 0, 0);
+        const v4i x = wload_s(drs, 0, k * 16);
+        return make_int4(x[0], x[1], x[2], x[3]);
+    };
+    // workgroup-uniform: scalar registers across the MLP
+    auto uniform = [](int4 x) {
+        return make_int4(__builtin_amdgcn_readfirstlane(x.x), __builtin_amdgcn_readfirstlane(x.y),
+                         __builtin_amdgcn_readfirstlane(x.z), __builtin_amdgcn_readfirstlane(x.w));
+    };
+    // Descriptors are loaded two tiles ahead, and the next tile's tokens are
+    // loaded right after this tile's MLP: both complete during this tile's
+    // epilogue (which waits for no memory load), so a tile starts without a
+    // memory round trip.
+    int4 d = uniform(desc_at((int32_t)blockIdx.x));
+    int v = (int32_t)blockIdx.x < n_tiles ? stage_token(d) : 0;
+    int4 dn = uniform(desc_at((int32_t)blockIdx.x + G));
+    for (int32_t tile = blockIdx.x; tile < n_tiles; tile += G) {
+        const int64_t base = (int64_t)(uint32_t)d.x | ((int64_t)d.y << 32);   // token t0 of the chunk
+        const int32_t rem = d.z;                                               // L - t0
         __syncthreads();
         if (threadIdx.x < R_TILE + WIN) {
             s_tok[threadIdx.x] = (uint16_t)v;
@@ -226,7 +252,8 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
         __syncthreads();
         mlp_tile<CORE, RT_TILE>(M, s_emb, s_act, s_par, [&](int r, int p) { return (int)s_apos[r + p]; },
                                 wave, lane);
-        if (tile + (int32_t)gridDim.x < n_tiles) d = desc[tile + gridDim.x];
+        const int vn = tile + G < n_tiles ? stage_token(dn) : 0;
+        const int4 dnn = desc_at(tile + 2 * G);
         uint2 *out = pairs + base;
         const int32_t valid = min(R_TILE, rem);
         // EPI_N row groups (gi + n * WAVES) per iteration, see row_freq.  The
@@ -256,6 +283,9 @@ __global__ __launch_bounds__(THREADS, 1) void k_compress_mlp(ModelDev M, const u
                 if (rr[n] < valid && (sym[n] & 15) == u) out[rr[n]] = make_uint2(cum, freq);
             }
         }
+        d = dn;
+        dn = uniform(dnn);
+        v = vn;
     }
 }
 
