@@ -230,6 +230,13 @@ struct EncArrays {
     int32_t *write_pos, *status;
 };
 
+static_assert(VOCAB == 256, "the step kernels stage one LUT entry per thread of a 256-thread workgroup");
+
+// The encode and decode steps issue every load a row needs (its logits,
+// its coder state, the LUT entry of the thread) before the LUT staging
+// barrier, so that a workgroup waits for one memory round trip instead of
+// three in a row (LUT, then logits, then state); a row's state is read
+// whether or not the step codes it (it lies inside the arrays either way).
 __global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ logits,
                                                      const uint64_t *__restrict__ lut,
                                                      const int64_t *__restrict__ symbols,
@@ -237,13 +244,25 @@ __global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ 
                                                      int64_t B, EncArrays st, uint32_t *__restrict__ words,
                                                      int64_t max_words) {
     __shared__ double s_lut[VOCAB];
-    stage_lut(lut, s_lut);
     const int u = threadIdx.x & 15;
     const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool in = b < B;
+    const v4i raw = global_logits16(logits, b, B, u);
+    const uint64_t lut_v = lut[threadIdx.x];   // 256 threads, VOCAB entries
+    int64_t vb = 0, sym = 0;
+    int32_t stb = 0;
+    EncState e{};
+    if (in) {
+        vb = valid[b];
+        sym = symbols[b];
+        stb = st.status[b];
+        e = EncState{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
+    }
+    s_lut[VOCAB - 1 - threadIdx.x] = (double)lut_v;   // reversed, as load_lut_lds
+    __syncthreads();
     Freq16 fr;
-    row_frequencies16(global_logits16(logits, b, B, u), s_lut, u, fr);
-    if (b >= B || t >= valid[b] || st.status[b]) return;
-    const int64_t sym = symbols[b];
+    row_frequencies16(raw, s_lut, u, fr);
+    if (!in || t >= vb || stb) return;
     if (sym < 0 || sym >= VOCAB) {
         if (u == 0) st.status[b] = SC_STATUS_BAD_TOKEN;
         return;
@@ -252,16 +271,17 @@ __global__ __launch_bounds__(256) void k_encode_step(const int8_t *__restrict__ 
     if ((s >> 4) != u) return;   // the lane holding the symbol runs the coder
     uint32_t cum, freq;
     freq16_at(fr, s & 15, cum, freq);
-    EncState e{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
-    if (enc_step(e, cum, freq, words + b * max_words, (int32_t)max_words)) {
-        st.status[b] = SC_STATUS_CAPACITY;
-        return;
-    }
+    // Every field goes back unconditionally, the status included (0 before
+    // this step, since the row is live): the state is unchanged when the step
+    // did not fit (enc_step).  One store per field and no branch between
+    // them, so that no store's address depends on the path taken.
+    const int full = enc_step(e, cum, freq, words + b * max_words, (int32_t)max_words);
     st.lower[b] = e.lower;
     st.range[b] = e.range;
     st.inverted[b] = e.inverted;
     st.first[b] = e.first;
     st.write_pos[b] = e.pos;
+    st.status[b] = full ? SC_STATUS_CAPACITY : SC_STATUS_OK;
 }
 
 __global__ __launch_bounds__(256) void k_encode_seal(int64_t B, EncArrays st, uint32_t *__restrict__ words,
@@ -293,18 +313,35 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
                                                      const uint32_t *__restrict__ words,
                                                      int64_t *__restrict__ symbols_out) {
     __shared__ double s_lut[VOCAB];
-    stage_lut(lut, s_lut);
     const int lane = threadIdx.x & 63, u = threadIdx.x & 15;
     const int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    Freq16 fr;
-    row_frequencies16(global_logits16(logits, b, B, u), s_lut, u, fr);
     const bool in_range = b < B;
-    const bool active = in_range && t < valid[b] && st.status[b] == 0;
+    const v4i raw = global_logits16(logits, b, B, u);
+    const uint64_t lut_v = lut[threadIdx.x];   // 256 threads, VOCAB entries
+    int64_t vb = 0, rp = 0, endp = 0;
+    int32_t stb = 0;
+    uint64_t lower0 = 0, range0 = ~0ull, point0 = 0;
+    if (in_range) {
+        vb = valid[b];
+        stb = st.status[b];
+        lower0 = st.lower[b];
+        range0 = st.range[b];
+        point0 = st.point[b];
+        rp = st.read_pos[b];
+        endp = st.end_pos[b];
+    }
+    s_lut[VOCAB - 1 - threadIdx.x] = (double)lut_v;   // reversed, as load_lut_lds
+    __syncthreads();
+    // the word a renormalisation would shift in, loaded during the frequency step
+    const uint32_t wnext = in_range && rp < endp ? words[rp] : 0u;
+    Freq16 fr;
+    row_frequencies16(raw, s_lut, u, fr);
+    const bool active = in_range && t < vb && stb == 0;
     uint64_t lower = 0, range = ~0ull, point = 0;
     if (active) {
-        lower = st.lower[b];
-        range = st.range[b];
-        point = st.point[b];
+        lower = lower0;
+        range = range0;
+        point = point0;
     }
     const uint64_t scale = range >> 24;
     uint32_t q = 0;
@@ -312,30 +349,29 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
     uint32_t cum, freq;
     const int sym = dec_symbol16(fr, q, lane, cum, freq);
     if (!in_range || u != 0) return;
-    if (!active) {
-        symbols_out[b] = VOCAB;
-        return;
+    // an inactive row returns symbol 256; an invalid stream keeps its state
+    // and records the status; otherwise the step's new state.  Every field
+    // of an active row goes back, the status included (0 before this step),
+    // with no branch between the stores.
+    const bool step = active && ok;
+    if (step) {
+        lower += scale * cum;
+        range = scale * freq;
+        if (range < (1ull << 32)) {
+            lower <<= 32;
+            range <<= 32;
+            point = (point << 32) | wnext;
+            rp += 1;
+        }
     }
-    if (!ok) {
-        st.status[b] = SC_STATUS_INVALID_STREAM;
-        symbols_out[b] = VOCAB;
-        return;
+    if (active) {
+        st.lower[b] = lower;
+        st.range[b] = range;
+        st.point[b] = point;
+        st.read_pos[b] = rp;
+        st.status[b] = ok ? SC_STATUS_OK : SC_STATUS_INVALID_STREAM;
     }
-    lower += scale * cum;
-    range = scale * freq;
-    int64_t rp = st.read_pos[b];
-    if (range < (1ull << 32)) {
-        lower <<= 32;
-        range <<= 32;
-        point <<= 32;
-        if (rp < st.end_pos[b]) point |= words[rp];
-        rp += 1;
-    }
-    st.lower[b] = lower;
-    st.range[b] = range;
-    st.point[b] = point;
-    st.read_pos[b] = rp;
-    symbols_out[b] = sym;
+    symbols_out[b] = step ? (int64_t)sym : (int64_t)VOCAB;
 }
 
 // ---- measurement: sustained int8 MFMA rate -------------------------------
