@@ -178,6 +178,69 @@ def test_step_api_many_streams(int_models, oracle_mod):
     dec.check()
 
 
+def test_step_encoder_capacity_per_stream(oracle_mod, int_models):
+    """Streams that fit max_words, that overflow at their seal (oracle word
+    count max_words + 1) and that overflow during a step, side by side:
+    each overflowing stream, and only it, reports SC_STATUS_CAPACITY;
+    every other stream's words equal the oracle's; get_compressed raises
+    OverflowError naming the first overflowing stream."""
+    from sigcomp_amd import _hip
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeStepEncoder
+    rng = np.random.default_rng(21)
+    lut_np = int_models["lossless"].exp_lut
+    B = 48
+    lens = rng.integers(1, 120, B)
+    T = int(lens.max())
+    lg = rng.normal(0, 20, (B, T, 256)).round().clip(-128, 127).astype(np.int8)
+    sy = rng.integers(0, 256, (B, T)).astype(np.int64)
+    totals = np.array([len(oracle_mod.encode_stream(lg[b, :lens[b]], sy[b, :lens[b]], lut_np)) for b in range(B)])
+    j = int(np.argsort(totals, kind="stable")[B // 2])
+    M = int(totals[j]) - 1                       # stream j's steps fit, its seal does not
+    over = totals > M
+    assert over.sum() >= 3 and (~over).sum() >= 3 and (totals >= M + 3).any()
+    enc = GpuRangeStepEncoder(B, M, device="cuda")
+    lg_d, sy_d = torch.from_numpy(lg).cuda(), torch.from_numpy(sy).cuda()
+    v_d = torch.from_numpy(lens.astype(np.int64)).cuda()
+    lut = torch.from_numpy(lut_np)
+    for t in range(T):
+        enc.encode_step_int8(lg_d[:, t], lut, sy_d[:, t], v_d, t)
+    enc.seal()
+    torch.cuda.synchronize()
+    status = enc.status.cpu().numpy()
+    assert np.array_equal(status != 0, over), (status, totals, M)
+    assert (status[over] == _hip.SC_STATUS_CAPACITY).all()
+    wp = enc.write_pos.cpu().numpy()
+    ow = enc.output_words.cpu().numpy().view(np.uint32)
+    for b in np.flatnonzero(~over):
+        ref = oracle_mod.encode_stream(lg[b, :lens[b]], sy[b, :lens[b]], lut_np)
+        assert np.array_equal(ow[b, :wp[b]], ref), b
+    with pytest.raises(OverflowError, match=f"stream {int(np.flatnonzero(over)[0])};"):
+        enc.get_compressed()
+
+
+def test_step_decoder_invalid_stream_beside_valid_ones(oracle_mod, int_models):
+    """A corrupt stream between valid ones: it returns 256 from the step
+    that detects it on (its status stays set), check() raises, and its
+    neighbours decode every symbol."""
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
+    rng = np.random.default_rng(22)
+    lut_np = int_models["lossless"].exp_lut
+    B, T = 5, 40
+    lg = rng.normal(0, 20, (B, T, 256)).round().clip(-128, 127).astype(np.int8)
+    sy = rng.integers(0, 256, (B, T)).astype(np.int64)
+    streams = [oracle_mod.encode_stream(lg[b], sy[b], lut_np).tobytes() for b in range(B)]
+    streams[2] = np.array([0xFFFFFFFF, 0xFFFFFFFF, 7], np.uint32).tobytes()
+    dec = GpuRangeDecoder(streams, device="cuda")
+    valid = torch.full((B,), T, dtype=torch.int64)
+    lg_d = torch.from_numpy(lg).cuda()
+    got = np.stack([dec.decode_step_int8(lg_d[:, t], lut_np, valid, t).cpu().numpy() for t in range(T)], axis=1)
+    for b in (0, 1, 3, 4):
+        assert np.array_equal(got[b], sy[b]), b
+    assert (got[2] == 256).all()
+    with pytest.raises(ValueError):
+        dec.check()
+
+
 def test_step_decoder_flags_invalid_stream(int_models):
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
     bad = np.array([0xFFFFFFFF, 0xFFFFFFFF], np.uint32).tobytes()
@@ -266,6 +329,45 @@ def test_compress_abi_negative_length_owns_no_tiles(codecs, oracle_mod, oracle_m
     assert not status.cpu().numpy().any() and c[1] == 0
     for i in range(n):
         assert w[word_off[i]:word_off[i] + c[i]].tobytes() == ref[i]
+
+
+def test_compress_abi_word_capacity_per_chunk(codecs, oracle_mod, oracle_models):
+    """Through the C ABI a caller sets each chunk's word capacity: chunks
+    whose capacity is exactly their oracle word count, one word short (the
+    seal does not fit) and half of it (a step does not fit), side by side.
+    Each short chunk, and only it, reports SC_STATUS_CAPACITY; every other
+    chunk's words equal the oracle's."""
+    from sigcomp_amd import _hip
+    codec = codecs["lossless"]
+    rng = np.random.default_rng(44)
+    lengths = np.array([300, 300, 300, 129, 129, 129, 2048, 2048, 1], np.int32)
+    chunks = [rng.integers(0, 60, n).astype(np.uint8) for n in lengths]
+    ref = oracle_mod.compress_chunks(oracle_models["lossless"], chunks)
+    need = np.array([len(r) // 4 for r in ref], np.int32)
+    cap = need.copy()
+    cap[[1, 4, 7]] -= 1                       # one word short
+    cap[[2, 5]] //= 2                         # half
+    short = cap < need
+    n = len(lengths)
+    n_tokens = int(lengths.sum())
+    tok_off = np.zeros(n, np.int64)
+    np.cumsum(lengths[:-1], out=tok_off[1:])
+    word_off = np.zeros(n, np.int64)
+    np.cumsum(cap[:-1].astype(np.int64), out=word_off[1:])
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_tok, t_off, t_len, t_woff, t_cap = d(np.concatenate(chunks)), d(tok_off), d(lengths), d(word_off), d(cap)
+    words, cnt, status, ws = codec._compress_buffers(n, n_tokens, int(cap.sum()))
+    L, p = _hip.lib(), _hip.ptr
+    _hip.check(L.sc_compress_chunks(codec.hip.handle, p(t_tok), p(t_off), p(t_len), n, n_tokens, p(words),
+                                    p(t_woff), p(t_cap), p(cnt), p(status), p(ws), ws.numel(),
+                                    torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    st, c = status.cpu().numpy(), cnt.cpu().numpy()
+    w = words.cpu().numpy().view(np.uint32)
+    assert np.array_equal(st != 0, short), (st, cap, need)
+    assert (st[short] == _hip.SC_STATUS_CAPACITY).all()
+    for i in np.flatnonzero(~short):
+        assert c[i] == need[i] and w[word_off[i]:word_off[i] + c[i]].tobytes() == ref[i], i
 
 
 def test_long_chunk_len_matches_oracle(int_models, oracle_mod, oracle_models):
