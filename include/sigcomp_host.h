@@ -65,7 +65,10 @@ int sc_host_split_fill(const int16_t *const *reads, const int64_t *len, int64_t 
  * small + small_off[r] and n_large[r] large values / gaps at large_off[r];
  * samples to out + out_off[r].  Fails for a read whose counts do not add up
  * to len - 1 or whose positions fall outside the read (the reference raises
- * IndexError / ValueError there). */
+ * IndexError / ValueError there).  A length below 1 fails with
+ * SC_HOST_ERR_EMPTY_READ before any read is rebuilt (out_off cannot place
+ * it); a read's positions are all checked before any of its samples is read
+ * or written. */
 int sc_host_reassemble(const int16_t *sig0, const int64_t *len, int64_t n_reads, int32_t lsb,
                        const uint8_t *small, const int64_t *small_off, const int64_t *n_small,
                        const uint16_t *large_adj, const uint32_t *large_gap, const int64_t *large_off,
@@ -91,7 +94,8 @@ int sc_host_frame(const uint32_t *words, const int64_t *word_off, const int32_t 
  * word_off[c] (absolute index into words_out), word_cnt[c] and tok_cnt[c] are
  * written.  Fails for a frame of zero bytes or of a byte count that is not a
  * multiple of four, a truncated frame, or trailing bytes after the last
- * frame. */
+ * frame.  A negative tokens[r] fails with SC_ERR_ARG (*bad = r) before
+ * anything is written. */
 int sc_host_parse(const uint8_t *data, const int64_t *data_off, const int64_t *data_len, const int64_t *tokens,
                   int64_t n_reads, int32_t chunk_len, const int64_t *chunk_begin, const int64_t *read_word_off,
                   uint32_t *words_out, int64_t *word_off, int32_t *word_cnt, int32_t *tok_cnt, int32_t n_threads,

@@ -192,6 +192,10 @@ def parse(payloads, tokens, chunk_len: int, n_threads: int = 0, words_out=None) 
     tokens = np.asarray(tokens, np.int64).reshape(-1)
     if len(tokens) != n:
         raise ValueError("Compressed read and token length counts differ")
+    if n and int(tokens.min()) < 0:
+        raise ValueError("token counts must be non-negative")
+    if int(chunk_len) < 1:
+        raise ValueError("chunk_len must be positive")
     data_len = np.fromiter((len(p) for p in payloads), np.int64, count=n)
     # each payload's own buffer, no joined copy: bytes objects through
     # c_char_p (their internal buffer), anything else as a uint8 view

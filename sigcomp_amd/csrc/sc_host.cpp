@@ -97,7 +97,7 @@ inline int16_t lossy_sample(int16_t s, int lsb) {
 // zigzag of the int16 delta b - a (np.diff on int16 wraps modulo 2**16)
 inline uint16_t zz_delta(int16_t a, int16_t b) {
     const int32_t d = (int16_t)(uint16_t)((uint32_t)(uint16_t)b - (uint32_t)(uint16_t)a);
-    return (uint16_t)(uint32_t)((d << 1) ^ (d >> 31));
+    return (uint16_t)(((uint32_t)d << 1) ^ (uint32_t)(d >> 31));
 }
 
 inline int16_t unzigzag(uint16_t z) {
@@ -120,6 +120,15 @@ int parse_reads(PayloadFn payload, const int64_t *data_len, const int64_t *token
         g_err = "bad argument";
         return SC_ERR_ARG;
     }
+    // a negative token count has no chunk layout (its chunk_begin would point
+    // the following reads' chunks outside the caller's arrays): refused
+    // before anything is written
+    for (int64_t r = 0; r < n_reads; ++r)
+        if (tokens[r] < 0) {
+            if (bad) *bad = r;
+            g_err = "negative token count";
+            return SC_ERR_ARG;
+        }
     FirstBad fb;
     parallel_for(n_reads, n_threads, [&](int64_t r) {
         const uint8_t *d = payload(r);
@@ -232,13 +241,18 @@ int sc_host_reassemble(const int16_t *sig0, const int64_t *len, int64_t n_reads,
         g_err = "bad argument";
         return SC_ERR_ARG;
     }
+    // an empty or negative length has no place in the output (the caller's
+    // out_off, a prefix sum of the lengths, would point the following reads
+    // outside `out`): refused before any sample is written
+    for (int64_t r = 0; r < n_reads; ++r)
+        if (len[r] < 1) {
+            if (bad) *bad = r;
+            g_err = std::string(err_text(SC_HOST_ERR_EMPTY_READ)) + " (item " + std::to_string(r) + ")";
+            return SC_HOST_ERR_EMPTY_READ;
+        }
     FirstBad fb;
     parallel_for(n_reads, n_threads, [&](int64_t r) {
         const int64_t n = len[r];
-        if (n < 1) {
-            fb.report(r, SC_HOST_ERR_EMPTY_READ);
-            return;
-        }
         if (n_small[r] < 0 || n_large[r] < 0 || n_small[r] + n_large[r] != n - 1) {
             fb.report(r, SC_HOST_ERR_COUNTS);
             return;
@@ -246,33 +260,34 @@ int sc_host_reassemble(const int16_t *sig0, const int64_t *len, int64_t n_reads,
         const uint8_t *sm = small + small_off[r];
         const uint16_t *la = large_adj + large_off[r];
         const uint32_t *lg = large_gap + large_off[r];
-        // positions: first gap, then gap + 1 steps; strictly increasing
-        int64_t next_large = n_large[r] ? (int64_t)lg[0] : INT64_MAX, k = 0;
-        if (n_large[r] && next_large >= n - 1) {
-            fb.report(r, SC_HOST_ERR_POSITION);
-            return;
+        // positions: first gap, then gap + 1 steps, so strictly increasing.
+        // All of them are checked against the read before any sample is
+        // rebuilt: the last one inside the read means every large value is
+        // placed, and the small values read are then exactly n_small.
+        int64_t last = -1;
+        for (int64_t k = 0; k < n_large[r]; ++k) {
+            last += (int64_t)lg[k] + 1;
+            if (last >= n - 1) {
+                fb.report(r, SC_HOST_ERR_POSITION);
+                return;
+            }
         }
+        int64_t next_large = n_large[r] ? (int64_t)lg[0] : INT64_MAX, k = 0;
         int16_t *o = out + out_off[r];
         int16_t v = sig0[r];
-        o[0] = lsb ? (int16_t)(uint16_t)(uint32_t)((int32_t)v << lsb) : v;
+        o[0] = lsb ? (int16_t)(uint16_t)((uint32_t)(int32_t)v << lsb) : v;
         int64_t js = 0;
         for (int64_t i = 0; i < n - 1; ++i) {
             uint16_t z;
             if (i == next_large) {
                 z = (uint16_t)(la[k] + 256u);
                 ++k;
-                if (k < n_large[r]) {
-                    next_large += (int64_t)lg[k] + 1;
-                    if (next_large >= n - 1) {
-                        fb.report(r, SC_HOST_ERR_POSITION);
-                        return;
-                    }
-                }
+                if (k < n_large[r]) next_large += (int64_t)lg[k] + 1;
             } else {
                 z = sm[js++];
             }
             v = (int16_t)(uint16_t)((uint32_t)(uint16_t)v + (uint32_t)(uint16_t)unzigzag(z));
-            o[i + 1] = lsb ? (int16_t)(uint16_t)(uint32_t)((int32_t)v << lsb) : v;
+            o[i + 1] = lsb ? (int16_t)(uint16_t)((uint32_t)(int32_t)v << lsb) : v;
         }
     });
     return finish(fb, bad);
