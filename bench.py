@@ -734,6 +734,9 @@ def bench_ceiling(args):
 #                    written (lower 8, range 8, inverted 4, first 4, pos 4)
 #   k_decode_step:   logits 256, valid 8, status 4, state read (lower, range,
 #                    point, read_pos, end_pos: 40) and written (32), symbol 8
+# from this many streams the library runs the encode / decode steps as its
+# wide kernels (64 rows per wave), below as the narrow ones
+STEP_WIDE_MIN_ROWS = 1 << 18
 CODER_BYTES = {"k_logits_to_cdf": 256 + 257 * 8, "k_encode_step": 256 + 8 + 8 + 4 + 2 * 28,
                "k_decode_step": 256 + 8 + 4 + 40 + 32 + 8}
 
@@ -819,7 +822,7 @@ def bench_coder(args):
             "vs_baseline": None, "dtype": "u64", "data": "synthetic",
             "config": {"workload": f"coder: {args.rows} streams x {T} steps of synthetic int8 logits "
                                    f"(and {20480} streams, the reference's batch)"},
-            "roofline": {"kernel": "k_decode_step", "bound": "hbm", "achieved": d["gb_s"], "peak": PEAK_HBM_GBS,
+            "roofline": {"kernel": "k_decode_step_wide" if args.rows >= STEP_WIDE_MIN_ROWS else "k_decode_step", "bound": "hbm", "achieved": d["gb_s"], "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": d["frac_of_hbm"], "traffic": None,
                          "algorithmic": f"{d['bytes_per_stream']} B per stream and step x {args.rows} streams"},
             "kernels": {str(B): v for B, v in out.items()}}

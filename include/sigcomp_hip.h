@@ -141,6 +141,9 @@ typedef struct {
 /* One encoder step for every stream b with t < valid_lens[b]: frequencies
  * from logits[b] (int8 [B, 256]) and the LUT, then the range-coder update
  * with symbols[b] (int64 [B]); words go to words[b * max_words + pos].
+ * From 2**18 streams the step runs as a kernel that codes 64 streams per
+ * wavefront (results identical; SC_HIP_STEP_WIDE=0 or 1 in the environment
+ * forces the small-batch or the large-batch kernel, as does sc_decode_step).
  * Replaces GpuRangeStepEncoder.encode_step_int8 / _range_encode_step_int8_kernel
  * (gpu_entropy_coding.py:270-280,137-252). */
 int sc_encode_step(const int8_t *logits, const uint64_t *lut, const int64_t *symbols,

@@ -374,6 +374,158 @@ __global__ __launch_bounds__(256) void k_decode_step(const int8_t *__restrict__ 
     symbols_out[b] = step ? (int64_t)sym : (int64_t)VOCAB;
 }
 
+// Large batches: the kernels above give each row 16 lanes for its frequency
+// table and then run the row's coder step (and the decoder's quantile) in
+// one of them, so that a wave's coder work uses 4 of its 64 lanes.  The wide
+// kernels give each wave 64 rows, in three phases: (A) one lane per row
+// loads the row's coder state (coalesced) and, in the decoder, computes its
+// quantile; (B) 16 passes of 4 rows, 16 lanes per row, compute the row's
+// frequencies and the coded symbol's (cum, freq) (the decoder's symbol
+// search), staged in LDS; (C) one lane per row runs the coder step and
+// stores the state.  Results are those of the narrow kernels, row by row.
+constexpr int WIDE_ROWS = 64;                      // rows per wave
+constexpr int WIDE_PASSES = WIDE_ROWS / 4;         // 4 rows per pass
+constexpr int64_t STEP_WIDE_MIN_ROWS = 1 << 18;   // below: the narrow kernels fill the GPU better
+
+__global__ __launch_bounds__(256) void k_encode_step_wide(const int8_t *__restrict__ logits,
+                                                          const uint64_t *__restrict__ lut,
+                                                          const int64_t *__restrict__ symbols,
+                                                          const int64_t *__restrict__ valid, int64_t t,
+                                                          int64_t B, EncArrays st, uint32_t *__restrict__ words,
+                                                          int64_t max_words) {
+    __shared__ double s_lut[VOCAB];
+    __shared__ uint32_t s_sym[4][WIDE_ROWS];   // the row's symbol, VOCAB when it takes no step
+    __shared__ uint32_t s_cum[4][WIDE_ROWS], s_freq[4][WIDE_ROWS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, u = lane & 15;
+    const int64_t base = ((int64_t)blockIdx.x * 4 + wave) * WIDE_ROWS;
+    const uint64_t lut_v = lut[threadIdx.x];   // 256 threads, VOCAB entries
+    // (A) lane = row
+    const int64_t b = base + lane;
+    const bool in = b < B;
+    int64_t vb = 0, sym = 0;
+    int32_t stb = 0;
+    EncState e{};
+    if (in) {
+        vb = valid[b];
+        sym = symbols[b];
+        stb = st.status[b];
+        e = EncState{st.lower[b], st.range[b], st.inverted[b], st.first[b], st.write_pos[b]};
+    }
+    const bool live = in && t < vb && stb == 0;
+    const bool bad = live && (sym < 0 || sym >= VOCAB);
+    s_sym[wave][lane] = live && !bad ? (uint32_t)sym : (uint32_t)VOCAB;
+    s_lut[VOCAB - 1 - threadIdx.x] = (double)lut_v;   // reversed, as load_lut_lds
+    __syncthreads();
+    // (B) 16 lanes per row, the next pass's logits loaded during this one
+    v4i raw = global_logits16(logits, base + (lane >> 4), B, u);
+#pragma unroll 1
+    for (int p = 0; p < WIDE_PASSES; ++p) {
+        const int r = 4 * p + (lane >> 4);
+        const v4i next = p + 1 < WIDE_PASSES ? global_logits16(logits, base + r + 4, B, u) : v4i{0, 0, 0, 0};
+        Freq16 fr;
+        row_frequencies16(raw, s_lut, u, fr);
+        const uint32_t s = s_sym[wave][r];
+        if (s < (uint32_t)VOCAB && (int)(s >> 4) == u) {
+            uint32_t cum, freq;
+            freq16_at(fr, (int)(s & 15), cum, freq);
+            s_cum[wave][r] = cum;
+            s_freq[wave][r] = freq;
+        }
+        raw = next;
+    }
+    slot_sync();   // this wave's LDS writes above, its reads below
+    // (C) lane = row; the stores as in k_encode_step
+    if (bad) st.status[b] = SC_STATUS_BAD_TOKEN;
+    if (!live || bad) return;
+    const int full = enc_step(e, s_cum[wave][lane], s_freq[wave][lane], words + b * max_words, (int32_t)max_words);
+    st.lower[b] = e.lower;
+    st.range[b] = e.range;
+    st.inverted[b] = e.inverted;
+    st.first[b] = e.first;
+    st.write_pos[b] = e.pos;
+    st.status[b] = full ? SC_STATUS_CAPACITY : SC_STATUS_OK;
+}
+
+__global__ __launch_bounds__(256) void k_decode_step_wide(const int8_t *__restrict__ logits,
+                                                          const uint64_t *__restrict__ lut,
+                                                          const int64_t *__restrict__ valid, int64_t t,
+                                                          int64_t B, DecArrays st,
+                                                          const uint32_t *__restrict__ words,
+                                                          int64_t *__restrict__ symbols_out) {
+    __shared__ double s_lut[VOCAB];
+    __shared__ uint32_t s_q[4][WIDE_ROWS];     // the row's quantile
+    __shared__ uint32_t s_sym[4][WIDE_ROWS], s_cum[4][WIDE_ROWS], s_freq[4][WIDE_ROWS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, u = lane & 15;
+    const int64_t base = ((int64_t)blockIdx.x * 4 + wave) * WIDE_ROWS;
+    const uint64_t lut_v = lut[threadIdx.x];   // 256 threads, VOCAB entries
+    // (A) lane = row: the state, the word a renormalisation would shift in,
+    // and the quantile (an inactive row's is unused)
+    const int64_t b = base + lane;
+    const bool in = b < B;
+    int64_t vb = 0, rp = 0, endp = 0;
+    int32_t stb = 0;
+    uint64_t lower = 0, range = ~0ull, point = 0;
+    if (in) {
+        vb = valid[b];
+        stb = st.status[b];
+        rp = st.read_pos[b];
+        endp = st.end_pos[b];
+    }
+    const bool active = in && t < vb && stb == 0;
+    if (active) {
+        lower = st.lower[b];
+        range = st.range[b];
+        point = st.point[b];
+    }
+    const uint32_t wnext = active && rp < endp ? words[rp] : 0u;
+    const uint64_t scale = range >> 24;
+    uint32_t q = 0;
+    const bool ok = scale != 0 && dec_quantile(point - lower, scale, q);
+    s_q[wave][lane] = q;
+    s_lut[VOCAB - 1 - threadIdx.x] = (double)lut_v;   // reversed, as load_lut_lds
+    __syncthreads();
+    // (B) 16 lanes per row: frequencies and the symbol search
+    v4i raw = global_logits16(logits, base + (lane >> 4), B, u);
+#pragma unroll 1
+    for (int p = 0; p < WIDE_PASSES; ++p) {
+        const int r = 4 * p + (lane >> 4);
+        const v4i next = p + 1 < WIDE_PASSES ? global_logits16(logits, base + r + 4, B, u) : v4i{0, 0, 0, 0};
+        Freq16 fr;
+        row_frequencies16(raw, s_lut, u, fr);
+        uint32_t cum, freq;
+        const int sym = dec_symbol16(fr, s_q[wave][r], lane, cum, freq);
+        if (u == 0) {
+            s_sym[wave][r] = (uint32_t)sym;
+            s_cum[wave][r] = cum;
+            s_freq[wave][r] = freq;
+        }
+        raw = next;
+    }
+    slot_sync();   // this wave's LDS writes above, its reads below
+    // (C) lane = row; the stores as in k_decode_step
+    if (!in) return;
+    const bool step = active && ok;
+    const uint32_t sym = s_sym[wave][lane];
+    if (step) {
+        lower += scale * s_cum[wave][lane];
+        range = scale * s_freq[wave][lane];
+        if (range < (1ull << 32)) {
+            lower <<= 32;
+            range <<= 32;
+            point = (point << 32) | wnext;
+            rp += 1;
+        }
+    }
+    if (active) {
+        st.lower[b] = lower;
+        st.range[b] = range;
+        st.point[b] = point;
+        st.read_pos[b] = rp;
+        st.status[b] = ok ? SC_STATUS_OK : SC_STATUS_INVALID_STREAM;
+    }
+    symbols_out[b] = step ? (int64_t)sym : (int64_t)VOCAB;
+}
+
 // ---- measurement: sustained int8 MFMA rate -------------------------------
 // Every wave runs 8 independent accumulator chains of v_mfma_i32_32x32x32_i8
 // on register operands (4 A and 4 B fragments of `ops`, rotated so that
@@ -782,6 +934,15 @@ int sc_logits_to_cdf(const int8_t *logits, int64_t rows, const uint64_t *lut, in
     return check_launch("k_logits_to_cdf");
 }
 
+// The wide step kernels for batches of at least STEP_WIDE_MIN_ROWS streams;
+// SC_HIP_STEP_WIDE = "0" / "1" forces the narrow / wide kernels (comparisons
+// and tests of both).
+static bool step_wide(int64_t B) {
+    const char *env = getenv("SC_HIP_STEP_WIDE");
+    if (env && (env[0] == '0' || env[0] == '1') && env[1] == 0) return env[0] == '1';
+    return B >= STEP_WIDE_MIN_ROWS;
+}
+
 static bool enc_ok(const sc_encoder_state *s) {
     return s && s->lower && s->range && s->inverted && s->first && s->write_pos && s->status;
 }
@@ -794,6 +955,11 @@ int sc_encode_step(const int8_t *logits, const uint64_t *lut, const int64_t *sym
     if (!logits || !lut || !symbols || !valid_lens || !words || !enc_ok(state))
         return fail(SC_ERR_ARG, "null device pointer");
     EncArrays a{state->lower, state->range, state->inverted, state->first, state->write_pos, state->status};
+    if (step_wide(B)) {
+        hipLaunchKernelGGL(k_encode_step_wide, dim3((unsigned)((B + 4 * WIDE_ROWS - 1) / (4 * WIDE_ROWS))), dim3(256),
+                           0, as_stream(stream), logits, lut, symbols, valid_lens, t, B, a, words, max_words);
+        return check_launch("k_encode_step_wide");
+    }
     hipLaunchKernelGGL(k_encode_step, dim3((unsigned)((B + 15) / 16)), dim3(256), 0, as_stream(stream), logits, lut,
                        symbols, valid_lens, t, B, a, words, max_words);
     return check_launch("k_encode_step");
@@ -817,6 +983,11 @@ int sc_decode_step(const int8_t *logits, const uint64_t *lut, const int64_t *val
         !state->point || !state->read_pos || !state->end_pos || !state->status || !words)
         return fail(SC_ERR_ARG, "null device pointer");
     DecArrays a{state->lower, state->range, state->point, state->read_pos, state->end_pos, state->status};
+    if (step_wide(B)) {
+        hipLaunchKernelGGL(k_decode_step_wide, dim3((unsigned)((B + 4 * WIDE_ROWS - 1) / (4 * WIDE_ROWS))), dim3(256),
+                           0, as_stream(stream), logits, lut, valid_lens, t, B, a, words, symbols_out);
+        return check_launch("k_decode_step_wide");
+    }
     hipLaunchKernelGGL(k_decode_step, dim3((unsigned)((B + 15) / 16)), dim3(256), 0, as_stream(stream), logits, lut,
                        valid_lens, t, B, a, words, symbols_out);
     return check_launch("k_decode_step");

@@ -116,8 +116,14 @@ def _golden_streams(name):
     return z, keys
 
 
+# "0" / "1": the narrow (16 lanes per row) / wide (64 rows per wave) step kernels
+STEP_PATHS = ["0", "1"]
+
+
+@pytest.mark.parametrize("wide", STEP_PATHS)
 @pytest.mark.parametrize("name", ["lossless", "lossy"])
-def test_step_encoder_and_decoder_match_reference(int_models, name):
+def test_step_encoder_and_decoder_match_reference(int_models, name, wide, monkeypatch):
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", wide)
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
     z, keys = _golden_streams(name)
     lut = torch.from_numpy(int_models[name].exp_lut)
@@ -148,11 +154,13 @@ def test_step_encoder_and_decoder_match_reference(int_models, name):
         assert np.all(got[b, valid[b]:] == 256)
 
 
-def test_step_api_many_streams(int_models, oracle_mod):
+@pytest.mark.parametrize("wide", STEP_PATHS)
+def test_step_api_many_streams(int_models, oracle_mod, wide, monkeypatch):
     """Large batches, as the coder benchmark runs them: 150,001 CDF rows
     (9,376 workgroups of 16 rows, the last one partial) against the oracle,
     and 70,001 streams x 3 encode / decode steps whose decoder returns every
     coded symbol, with every 1000th stream active for one step only."""
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", wide)
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder, int8_logits_to_cdf
     lut_np = int_models["lossless"].exp_lut
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -178,12 +186,54 @@ def test_step_api_many_streams(int_models, oracle_mod):
     dec.check()
 
 
-def test_step_encoder_capacity_per_stream(oracle_mod, int_models):
+def test_step_api_wide_batch_default_path_against_oracle(int_models, oracle_mod, monkeypatch):
+    """A batch at the size from which the wide step kernels are chosen
+    (2**18 streams + 1: 1,025 workgroups of 256 rows, the last with one),
+    5 steps with stream lengths from 1 to 5: 64 streams' sealed words
+    against the oracle, the decoder returns every coded symbol, and the
+    narrow kernels give the same words."""
+    monkeypatch.delenv("SC_HIP_STEP_WIDE", raising=False)
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
+    lut_np = int_models["lossless"].exp_lut
+    lut = torch.from_numpy(lut_np)
+    B, T = (1 << 18) + 1, 5
+    g = torch.Generator(device="cuda").manual_seed(8)
+    lg = (torch.randn(T, B, 256, generator=g, device="cuda") * 20).round().clamp(-128, 127).to(torch.int8)
+    sy = torch.randint(0, 256, (T, B), generator=g, device="cuda")
+    valid = torch.randint(1, T + 1, (B,), generator=g, device="cuda")
+    valid[-1] = T
+
+    def encode():
+        enc = GpuRangeStepEncoder(B, T + 32, device="cuda")
+        for t in range(T):
+            enc.encode_step_int8(lg[t], lut, sy[t], valid, t)
+        return enc.get_compressed()
+
+    words = encode()
+    rng = np.random.default_rng(9)
+    pick = np.r_[rng.choice(B - 1, 63, replace=False), B - 1]
+    lg_h, sy_h, v_h = lg.cpu().numpy(), sy.cpu().numpy(), valid.cpu().numpy()
+    for b in pick:
+        n = int(v_h[b])
+        ref = oracle_mod.encode_stream(lg_h[:n, b], sy_h[:n, b], lut_np)
+        assert np.array_equal(np.frombuffer(words[b], "<u4"), ref), b
+    dec = GpuRangeDecoder(words, device="cuda")
+    for t in range(T):
+        got = dec.decode_step_int8(lg[t], lut, valid, t).clone()
+        assert torch.equal(got, torch.where(valid > t, sy[t], torch.full_like(sy[t], 256))), t
+    dec.check()
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", "0")
+    assert encode() == words
+
+
+@pytest.mark.parametrize("wide", STEP_PATHS)
+def test_step_encoder_capacity_per_stream(oracle_mod, int_models, wide, monkeypatch):
     """Streams that fit max_words, that overflow at their seal (oracle word
     count max_words + 1) and that overflow during a step, side by side:
     each overflowing stream, and only it, reports SC_STATUS_CAPACITY;
     every other stream's words equal the oracle's; get_compressed raises
     OverflowError naming the first overflowing stream."""
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", wide)
     from sigcomp_amd import _hip
     from sigcomp_amd.gpu_entropy_coding import GpuRangeStepEncoder
     rng = np.random.default_rng(21)
@@ -218,10 +268,12 @@ def test_step_encoder_capacity_per_stream(oracle_mod, int_models):
         enc.get_compressed()
 
 
-def test_step_decoder_invalid_stream_beside_valid_ones(oracle_mod, int_models):
+@pytest.mark.parametrize("wide", STEP_PATHS)
+def test_step_decoder_invalid_stream_beside_valid_ones(oracle_mod, int_models, wide, monkeypatch):
     """A corrupt stream between valid ones: it returns 256 from the step
     that detects it on (its status stays set), check() raises, and its
     neighbours decode every symbol."""
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", wide)
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
     rng = np.random.default_rng(22)
     lut_np = int_models["lossless"].exp_lut
@@ -241,7 +293,9 @@ def test_step_decoder_invalid_stream_beside_valid_ones(oracle_mod, int_models):
         dec.check()
 
 
-def test_step_decoder_flags_invalid_stream(int_models):
+@pytest.mark.parametrize("wide", STEP_PATHS)
+def test_step_decoder_flags_invalid_stream(int_models, wide, monkeypatch):
+    monkeypatch.setenv("SC_HIP_STEP_WIDE", wide)
     from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder
     bad = np.array([0xFFFFFFFF, 0xFFFFFFFF], np.uint32).tobytes()
     dec = GpuRangeDecoder([bad], device="cuda")
