@@ -932,6 +932,61 @@ def test_split_decode_corrupt_chunks(codecs, monkeypatch):
             assert np.array_equal(back[s], tokens[s]), i
 
 
+@pytest.mark.parametrize("split", ["0", None])
+def test_decode_of_garbage_and_damaged_chunks_matches_oracle(codecs, oracle_mod, oracle_models, monkeypatch, split):
+    """Arbitrary words are a range-coded stream too: the decoder either
+    reaches a quantile outside the table (an invalid stream) or returns
+    tokens.  Over 600 chunks (lengths 1-150) of three kinds side by side
+    -- valid streams, 0 to 8 random words, and valid streams cut short or
+    with one word changed -- plus five streams invalid at their first step,
+    each chunk's status, and the tokens of every chunk that decodes, equal
+    the C oracle's; with the persistent decode
+    (split "0") and with the default plan, a split decode for this batch."""
+    import ctypes
+    codec = codecs["lossless"]
+    rng = np.random.default_rng(600 if split is None else 601)
+    n = 600
+    lengths = rng.integers(1, 151, n).astype(np.int32)
+    tokens = rng.integers(0, 60, int(lengths.sum())).astype(np.uint8)
+    words, woff, wcnt = codec.compress_flat(tokens, lengths)
+    streams = [words[woff[i]:woff[i] + wcnt[i]].copy() for i in range(n)]
+    kind = rng.integers(0, 3, n)
+    for i in np.flatnonzero(kind == 1):
+        streams[i] = rng.integers(0, 1 << 32, rng.integers(0, 9), dtype=np.uint64).astype(np.uint32)
+    for i in np.flatnonzero(kind == 2):
+        s = streams[i]
+        if len(s) > 1 and rng.random() < 0.5:
+            streams[i] = s[:rng.integers(0, len(s))]
+        else:
+            s[rng.integers(0, len(s))] ^= np.uint32(1 << int(rng.integers(0, 32)))
+    # (almost any words decode: a point outside the coder's range is rare)
+    # five streams whose first step's quantile is outside the table
+    bad = rng.choice(n, 5, replace=False)
+    for i in bad:
+        streams[i] = np.array([0xFFFFFFFF, 0xFFFFFFFF, 7], np.uint32)
+    cnt = np.array([len(s) for s in streams], np.int32)
+    off = np.zeros(n, np.int64)
+    np.cumsum(cnt[:-1], dtype=np.int64, out=off[1:])
+    flat = np.concatenate(streams + [np.zeros(1, np.uint32)])
+    if split is None:
+        monkeypatch.delenv("SC_HIP_DEC_SPLIT", raising=False)
+    else:
+        monkeypatch.setenv("SC_HIP_DEC_SPLIT", split)
+    back, status, tok_off = _decode_direct(codec, flat, off, cnt, lengths)
+    # the oracle, every chunk's status (its Python wrapper raises on the first)
+    om = oracle_models["lossless"]
+    ref_tok = np.zeros(int(lengths.sum()), np.uint8)
+    ref_status = np.zeros(n, np.int32)
+    oracle_mod.lib().sco_decompress_chunks(ctypes.byref(om.c), om.lut, flat, off, cnt, lengths, n, ref_tok,
+                                           tok_off, ref_status)
+    assert (status[bad] == 2).all()
+    assert np.array_equal(status != 0, ref_status != 0), np.flatnonzero((status != 0) != (ref_status != 0))
+    assert set(np.unique(status)) <= {0, 2}   # SC_STATUS_OK, SC_STATUS_INVALID_STREAM
+    for i in np.flatnonzero(status == 0):
+        s = slice(tok_off[i], tok_off[i] + lengths[i])
+        assert np.array_equal(back[s], ref_tok[s]), i
+
+
 def test_split_decode_timeout_reports_status_and_redecodes_unsplit(codecs, monkeypatch):
     """With a spin limit of 0 polls (SC_HIP_DEC_SPIN=0; the default is
     2**18) every wait of a split decode gives up at once: every chunk of
