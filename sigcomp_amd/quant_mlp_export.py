@@ -411,7 +411,7 @@ class QuantMLPCompression(ReadFramingMixin):
             raise ValueError("Compressed chunk and length counts differ")
         if n and (np.any(lengths < 0) or np.any(lengths > self.chunk_len)):
             raise ValueError("Chunk lengths must be integers in [0, chunk_len]")
-        if n and (np.any(word_off < 0) or np.any(word_off + cnt > len(words))
+        if n and (np.any(word_off < 0) or np.any(cnt < 0) or np.any(word_off + cnt > len(words))
                   or np.any((lengths > 0) & (cnt == 0)) or np.any((lengths == 0) & (cnt > 0))):
             raise ValueError("Invalid range-coded chunk for its token length")
         tok_off = np.zeros(n, dtype=np.int64)

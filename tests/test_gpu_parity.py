@@ -460,6 +460,21 @@ def test_decompress_corrupt_chunk_raises(codecs):
         codecs["lossless"].decompress_chunks(bad, [10])
 
 
+def test_decompress_flat_rejects_inconsistent_chunk_tables(codecs):
+    """Word ranges outside the word array (negative offset or count, past
+    its end), words for an empty chunk or none for a non-empty one, a length
+    beyond chunk_len: ValueError before anything reaches the GPU."""
+    codec = codecs["lossless"]
+    words = np.arange(10, dtype=np.uint32)
+    cases = [([0, -1], [4, 6], [5, 7], "Invalid range-coded"), ([0, 4], [4, -2], [5, 7], "Invalid range-coded"),
+             ([0, 4], [4, 7], [5, 7], "Invalid range-coded"), ([0, 4], [4, 0], [5, 7], "Invalid range-coded"),
+             ([0, 4], [4, 6], [5, 0], "Invalid range-coded"), ([0, 4], [4, 6], [5, codec.chunk_len + 1], "chunk_len"),
+             ([0], [4, 6], [5, 7], "counts differ")]
+    for woff, cnt, lengths, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            codec.decompress_flat(words, np.array(woff, np.int64), np.array(cnt, np.int32), np.array(lengths, np.int32))
+
+
 def test_empty_inputs(codecs):
     assert codecs["lossless"].compress_chunks([]) == []
     assert codecs["lossless"].decompress_chunks([], []) == []
