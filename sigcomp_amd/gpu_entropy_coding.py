@@ -193,6 +193,8 @@ class GpuRangeDecoder:
             raise ValueError("t must be nonnegative")
         logits = int8_logits.to(self.device).contiguous()
         valid = torch.as_tensor(valid_lens_tensor).to(self.device, torch.int64).contiguous()
+        if valid.shape != (self.B,):
+            raise ValueError("valid_lens must have shape (batch,)")
         lut = _lut_on(exp_lut, self.device)
         with torch.cuda.device(self.device):
             _hip.check(_hip.lib().sc_decode_step(

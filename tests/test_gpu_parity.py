@@ -306,6 +306,33 @@ def test_step_decoder_flags_invalid_stream(int_models, wide, monkeypatch):
         dec.check()
 
 
+def test_step_api_rejects_mis_shaped_arguments(int_models):
+    """Per-stream arguments whose length is not the batch size (the kernels
+    index them by stream) and logits of the wrong shape or dtype: ValueError
+    before any launch, on the encoder and the decoder."""
+    from sigcomp_amd.gpu_entropy_coding import GpuRangeDecoder, GpuRangeStepEncoder
+    lut = int_models["lossless"].exp_lut
+    B = 5
+    lg = torch.zeros((B, 256), dtype=torch.int8, device="cuda")
+    enc = GpuRangeStepEncoder(B, 8, device="cuda")
+    sy = torch.zeros(B, dtype=torch.int64)
+    ok = torch.full((B,), 3)
+    for bad_sy, bad_valid in ((sy[:-1], ok), (sy, ok[:-1]), (sy, torch.full((B + 1,), 3))):
+        with pytest.raises(ValueError):
+            enc.encode_step_int8(lg, lut, bad_sy, bad_valid, 0)
+    with pytest.raises(ValueError):
+        enc.encode_step_int8(lg[:-1], lut, sy, ok, 0)
+    with pytest.raises(ValueError):
+        enc.encode_step_int8(lg.to(torch.int16), lut, sy, ok, 0)
+    dec = GpuRangeDecoder([np.zeros(2, np.uint32).tobytes()] * B, device="cuda")
+    for bad_valid in (ok[:-1], torch.full((B + 1,), 3), torch.full((B, 1), 3)):
+        with pytest.raises(ValueError):
+            dec.decode_step_int8(lg, lut, bad_valid, 0)
+    with pytest.raises(ValueError):
+        dec.decode_step_int8(lg[:-1], lut, ok, 0)
+    assert dec.decode_step_int8(lg, lut, ok, 0).shape == (B,)
+
+
 @pytest.mark.parametrize("name", ["lossless", "lossy"])
 def test_batch_inference_reads_matches_reference_e2e(codecs, name):
     from sigcomp_amd import signal
