@@ -502,6 +502,31 @@ def test_decompress_flat_rejects_inconsistent_chunk_tables(codecs):
             codec.decompress_flat(words, np.array(woff, np.int64), np.array(cnt, np.int32), np.array(lengths, np.int32))
 
 
+@pytest.mark.parametrize("name", ["lossless", "lossy"])
+def test_full_symbol_range_against_oracle(codecs, oracle_mod, oracle_models, monkeypatch, name):
+    """Tokens uniform over all 256 symbols (most of them rare under the
+    model: frequencies at the floor of 1, ~3 bytes of stream per token), and
+    chunks of only 255 or only 0: every chunk's bytes equal the oracle's and
+    both the persistent and the split decode return the tokens."""
+    codec = codecs[name]
+    rng = np.random.default_rng(256 + (name == "lossy"))
+    lengths = rng.integers(1, 301, 200).astype(np.int32)
+    lengths[:4] = [1, 64, 300, 2048]
+    chunks = [rng.integers(0, 256, n).astype(np.uint8) for n in lengths]
+    chunks[0][:] = 255
+    chunks[1][:] = 255
+    chunks[2][:] = 0
+    comp = codec.compress_chunks(chunks)
+    assert comp == oracle_mod.compress_chunks(oracle_models[name], chunks)
+    for split in ("0", None):
+        if split is None:
+            monkeypatch.delenv("SC_HIP_DEC_SPLIT", raising=False)
+        else:
+            monkeypatch.setenv("SC_HIP_DEC_SPLIT", split)
+        back = codec.decompress_chunks(comp, list(lengths))
+        assert all(np.array_equal(a, b) for a, b in zip(chunks, back)), split
+
+
 def test_empty_inputs(codecs):
     assert codecs["lossless"].compress_chunks([]) == []
     assert codecs["lossless"].decompress_chunks([], []) == []
