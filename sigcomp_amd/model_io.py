@@ -114,9 +114,9 @@ def make_layer(weight, bias, m0, shift, relu) -> IntLayer:
     m0 = _per_channel(m0, n, np.int64)
     shift = _per_channel(shift, n, np.int32)
     if np.any(m0 < 0) or np.any(m0 > (1 << 31)):
-        raise ValueError("The quantized multiplier must be in [0, 2**31]")
+        raise ValueError("requantisation multiplier m0 outside [0, 2**31]")
     if np.any(shift < 0) or np.any(shift > 63):
-        raise ValueError("The quantized right shift must be in [0, 63]")
+        raise ValueError("requantisation shift outside [0, 63]")
     return IntLayer(weight, bias, m0, shift, bool(relu))
 
 
@@ -130,9 +130,9 @@ def _from_pth(path, dim, num_dec_layers, window_size) -> IntModel:
         embedding = state["decoder.embedding_linear.weight"]
         input_scale = float(state["decoder.quant.scale"].item())
         if tuple(embedding.shape) != (257, dim // 2):
-            raise ValueError("Checkpoint embedding shape does not match --dim")
+            raise ValueError("embedding width of the checkpoint is not --dim / 2")
         if not math.isfinite(input_scale) or input_scale <= 0:
-            raise ValueError("Invalid embedding quantization scale")
+            raise ValueError("embedding scale of the checkpoint is not a positive finite number")
         emb = torch.round(embedding / input_scale).clamp(-128, 127).to(torch.int8).numpy()
         layers = []
         s_in = input_scale
@@ -143,12 +143,12 @@ def _from_pth(path, dim, num_dec_layers, window_size) -> IntModel:
             output_scale = float(state[f"{prefix}.scale"].item())
             output_width = dim * 2 if index < num_dec_layers else VOCAB_SIZE
             if tuple(weight.shape) != (output_width, expected_input):
-                raise ValueError(f"Checkpoint {prefix} shape does not match the architecture")
+                raise ValueError(f"{prefix}: weight shape disagrees with the requested architecture")
             if not math.isfinite(output_scale) or output_scale <= 0:
-                raise ValueError(f"Invalid quantization scale for {prefix}")
+                raise ValueError(f"{prefix}: scale is not a positive finite number")
             if weight.dtype != torch.qint8 or weight.qscheme() not in (
                     torch.per_tensor_affine, torch.per_tensor_symmetric):
-                raise ValueError("Expected per-tensor quantized int8 linear weights")
+                raise ValueError("linear weights must be int8 with one (per-tensor) scale")
             bias_scale = s_in * weight.q_scale()
             if bias is None:
                 bias_q = np.zeros(output_width, dtype=np.int32)
@@ -162,7 +162,7 @@ def _from_pth(path, dim, num_dec_layers, window_size) -> IntModel:
         n_packed = sum(k.startswith("decoder.mlp.") and k.endswith("._packed_params._packed_params")
                        for k in state)
         if n_packed != num_dec_layers + 1:
-            raise ValueError("Checkpoint layer count does not match --num-dec-layers")
+            raise ValueError("number of checkpoint layers disagrees with --num-dec-layers")
     except KeyError as exc:
         raise ValueError(f"Incomplete or incompatible quantized MLP checkpoint: {exc}") from exc
     # output_scale buffer is float32 in both reference decoders
@@ -203,13 +203,13 @@ def _from_npz(path, dim, num_dec_layers, window_size) -> IntModel:
                          input_scale=float(z["input_scale"]),
                          exp_lut=np.ascontiguousarray(z["exp_lut"]))
     if model.emb.ndim != 2 or model.emb.shape != (SOS_TOKEN + 1, dim // 2):
-        raise ValueError("Checkpoint embedding shape does not match --dim")
+        raise ValueError("embedding width of the checkpoint is not --dim / 2")
     if len(model.layers) != num_dec_layers + 1:
-        raise ValueError("Checkpoint layer count does not match --num-dec-layers")
+        raise ValueError("number of checkpoint layers disagrees with --num-dec-layers")
     if any(layer.n != dim * 2 for layer in model.layers[:-1]):
-        raise ValueError("Checkpoint hidden width does not match --dim")
+        raise ValueError("hidden width of the checkpoint is not --dim")
     if window_size is not None and int(window_size) != model.window:
-        raise ValueError("Model window size does not match --window-size")
+        raise ValueError("context window of the model is not --window-size")
     return model
 
 
@@ -219,7 +219,7 @@ def load_int_model(model_path=None, dim=None, num_dec_layers=None, window_size=N
     dim = 256 if dim is None else int(dim)
     num_dec_layers = 8 if num_dec_layers is None else int(num_dec_layers)
     if dim < 2 or num_dec_layers < 0 or (window_size is not None and int(window_size) < 1):
-        raise ValueError("Invalid MLP architecture")
+        raise ValueError("dim must be at least 2, num_dec_layers at least 0 and window_size at least 1")
     if path.suffix == ".npz":
         model = _from_npz(path, dim, num_dec_layers, window_size)
     else:

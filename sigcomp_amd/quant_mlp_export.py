@@ -119,7 +119,7 @@ class HipModel:
     def forward_windows(self, ctx: torch.Tensor, out: str = "logits") -> torch.Tensor:
         """ctx int64 [rows, window] (device) -> int8 logits [rows, 256] or int32 CDF [rows, 257]."""
         if ctx.ndim != 2 or ctx.shape[1] != self.window:
-            raise ValueError("context_window must be shaped [batch, window_size]")
+            raise ValueError("context windows must be a [rows, window_size] tensor")
         ctx = ctx.to(self.device, torch.int64).contiguous()
         rows = ctx.shape[0]
         status = torch.zeros(1, dtype=torch.int32, device=self.device)
